@@ -1,0 +1,174 @@
+// Device-side helpers shared by every nano-vllm-rs fused kernel on gfx950.
+//
+// Numerics contract (all sources are compiled with -ffp-contract=off, so every
+// a*b+c below is two roundings unless written as __builtin_fmaf):
+//  * bf16 is the upper half of an IEEE binary32; widening is exact and
+//    narrowing is round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
+//  * nvr_logf is a deterministic logarithm (range reduction to
+//    [sqrt(1/2), sqrt(2)) plus a degree-8 polynomial evaluated with explicit
+//    FMAs). It uses only correctly rounded IEEE operations, so the host oracle
+//    reproduces it bit for bit; its error is below 1 ulp over all positive
+//    normal floats.
+//  * The RoPE angle helpers evaluate pow/sin/cos in binary64 with fixed
+//    operation sequences, again reproducible on the host.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nvr {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16 ----
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+}
+// Two floats -> two bf16 in one dword (lo in bits 0..15), round to nearest even.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+}
+// Widen 8 packed bf16 (one 16-byte load) into floats.
+__device__ __forceinline__ void unpack8(const uint4& w, float* f) {
+    f[0] = bf16_lo(w.x); f[1] = bf16_hi(w.x);
+    f[2] = bf16_lo(w.y); f[3] = bf16_hi(w.y);
+    f[4] = bf16_lo(w.z); f[5] = bf16_hi(w.z);
+    f[6] = bf16_lo(w.w); f[7] = bf16_hi(w.w);
+}
+__device__ __forceinline__ uint4 pack8(const float* f) {
+    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]),
+                      pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+}
+
+// Round a float to bf16 precision and widen it back (the value a bf16 store
+// followed by a load would produce).
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+// -------------------------------------------------------- cross-lane ops ----
+// Butterfly exchange with lane ^ mask inside a wave64. For an IEEE sum the
+// butterfly leaves every lane with the same bits as the down-shift tree's
+// lane 0, because each level adds the same two operands (a+b == b+a).
+__device__ __forceinline__ float xor_lane(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+__device__ __forceinline__ int xor_lane(int v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// ------------------------------------------------------------- 1 / sqrt ----
+// Correctly rounded sqrt followed by a correctly rounded division: fixed bits
+// on host and device. HIP keeps fp32 `/` and sqrtf correctly rounded by
+// default (v_sqrt_f32 plus a residual-based fix-up); __fsqrt_rn lowers to the
+// bare v_sqrt_f32 and is deliberately not used.
+__device__ __forceinline__ float inv_sqrt_rn(float x) { return 1.0f / sqrtf(x); }
+
+// ------------------------------------------------------------- logarithm ----
+// ln(x) for positive normal x. x = 2^e * m with m in [sqrt(1/2), sqrt(2));
+// f = m - 1 is exact; ln(1+f) = f + f^2 * Q(f) with Q a degree-8 fit of
+// (ln(1+f) - f) / f^2; ln x = e*ln2_hi + (e*ln2_lo + ln(1+f)).
+__device__ __forceinline__ float nvr_logf(float x) {
+    const uint32_t ix = __float_as_uint(x);
+    int32_t e = int32_t(ix >> 23) - 127;
+    const uint32_t mb = ix & 0x7fffffu;
+    const bool big = mb >= 0x3504f3u;  // m >= sqrt(2): halve m, bump e
+    const float m = __uint_as_float(mb | (big ? 0x3f000000u : 0x3f800000u));
+    e += big ? 1 : 0;
+    const float f = m - 1.0f;
+    const float z = f * f;
+    float q = -0x1.38dc50p-4f;                   // c8
+    q = __builtin_fmaf(q, f, 0x1.087188p-3f);    // c7
+    q = __builtin_fmaf(q, f, -0x1.0f27e8p-3f);   // c6
+    q = __builtin_fmaf(q, f, 0x1.2269fep-3f);    // c5
+    q = __builtin_fmaf(q, f, -0x1.542872p-3f);   // c4
+    q = __builtin_fmaf(q, f, 0x1.99a462p-3f);    // c3
+    q = __builtin_fmaf(q, f, -0x1.000422p-2f);   // c2
+    q = __builtin_fmaf(q, f, 0x1.555550p-2f);    // c1
+    q = __builtin_fmaf(q, f, -0x1.fffff8p-2f);   // c0
+    const float r = __builtin_fmaf(z, q, f);
+    const float ef = float(e);
+    return __builtin_fmaf(ef, 0x1.62e430p-1f, __builtin_fmaf(ef, -0x1.05c610p-29f, r));
+}
+
+// ------------------------------------------------------------- sampling ----
+// SplitMix64 finaliser (Steele, Lea, Flood 2014; constants by Vigna).
+__device__ __forceinline__ uint64_t splitmix64(uint64_t v) {
+    v += 0x9e3779b97f4a7c15ull;
+    v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ull;
+    v = (v ^ (v >> 27)) * 0x94d049bb133111ebull;
+    return v ^ (v >> 31);
+}
+constexpr uint64_t kTokenMix = 0xd2b74407b1ce6e93ull;
+
+// Uniform in (0,1) from the top 23 hash bits: (k + 0.5) * 2^-23, exact in fp32.
+__device__ __forceinline__ float hash_uniform(uint64_t r) {
+    return (float(uint32_t(r >> 41)) + 0.5f) * (1.0f / 8388608.0f);
+}
+// Gumbel-max score of one vocabulary entry: logit / T - ln(-ln(u)).
+__device__ __forceinline__ float gumbel_score(float logit, float temperature, uint64_t seed, uint32_t token) {
+    const uint64_t r = splitmix64(seed ^ (uint64_t(token) * kTokenMix));
+    const float u = hash_uniform(r);
+    return logit / temperature - nvr_logf(-nvr_logf(u));
+}
+
+// Total order used by every argmax: higher score wins, equal scores go to the
+// lower index, NaN never wins (all comparisons with NaN are false).
+__device__ __forceinline__ bool better(float s, int i, float best, int best_i) {
+    return s > best || (s == best && i < best_i);
+}
+constexpr int kNoIndex = 0x7fffffff;
+
+// ------------------------------------------------------- RoPE frequencies ----
+// Binary64 helpers with fixed operation order; only used to build the cos/sin
+// values of one (position, pair), so speed is secondary to reproducibility.
+__device__ __forceinline__ double d_log(double x) {
+    // x > 0 normal. x = 2^k * m, m in [sqrt(1/2), sqrt(2)); ln m = 2 atanh(s).
+    int k;
+    double m = frexp(x, &k);  // m in [0.5, 1)
+    if (m < 0.70710678118654752440) { m *= 2.0; k -= 1; }
+    const double s = (m - 1.0) / (m + 1.0);
+    const double s2 = s * s;
+    double t = 1.0 / 25.0;
+    for (int n = 23; n >= 1; n -= 2) t = t * s2 + 1.0 / double(n);
+    const double kd = double(k);
+    return kd * 0x1.62e42fee00000p-1 + (kd * 0x1.a39ef35793c76p-33 + 2.0 * s * t);
+}
+__device__ __forceinline__ double d_exp(double y) {
+    const double kd = floor(y * 0x1.71547652b82fep+0 + 0.5);
+    const double r = (y - kd * 0x1.62e42fee00000p-1) - kd * 0x1.a39ef35793c76p-33;
+    double t = 1.0;
+    for (int n = 18; n >= 1; --n) t = 1.0 + t * r / double(n);
+    return ldexp(t, int(kd));
+}
+__device__ __forceinline__ void d_sincos(double a, double* s, double* c) {
+    const double kd = floor(a * 0x1.45f306dc9c883p-1 + 0.5);
+    const double r = ((a - kd * 0x1.921fb54400000p+0) - kd * 0x1.0b4611a600000p-34) - kd * 0x1.3198a2e037073p-69;
+    const double r2 = r * r;
+    double ts = 0.0, tc = 0.0;
+    // sin r = r * sum (-r^2)^n / (2n+1)!, cos r = sum (-r^2)^n / (2n)!, n <= 11
+    double fs = 1.0, fc = 1.0;
+    for (int n = 11; n >= 1; --n) {
+        fs = 1.0 - fs * r2 / double((2 * n) * (2 * n + 1));
+        fc = 1.0 - fc * r2 / double((2 * n - 1) * (2 * n));
+    }
+    ts = r * fs;
+    tc = fc;
+    const long long q = (long long)kd & 3;
+    if (q == 0) { *s = ts; *c = tc; }
+    else if (q == 1) { *s = tc; *c = -ts; }
+    else if (q == 2) { *s = -ts; *c = -tc; }
+    else { *s = -tc; *c = ts; }
+}
+// cos/sin of position * theta^(-2*pair/dim), with the exponent, the power and
+// the angle each rounded to fp32 as the reference forms them, and cos/sin
+// evaluated in binary64 then rounded to fp32.
+__device__ __forceinline__ void rope_cos_sin(int position, int pair, int dim, float theta, float* c, float* s) {
+    const float expo = -float(2 * pair) / float(dim);
+    const float inv_freq = float(d_exp(double(expo) * d_log(double(theta))));
+    const float angle = float(position) * inv_freq;
+    double sd, cd;
+    d_sincos(double(angle), &sd, &cd);
+    *c = float(cd);
+    *s = float(sd);
+}
+
+}  // namespace nvr

@@ -1,0 +1,41 @@
+// Host-side internals of the nano-vllm-rs HIP library: the context object,
+// status plumbing and launch checks shared by every translation unit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hipblas/hipblas.h>
+#include <stdint.h>
+
+struct nv_context {
+    int device;
+    hipStream_t stream;
+    hipblasHandle_t blas;
+    int cu_count;
+};
+
+namespace nvr {
+
+// Records "<operation>: <message> (<code>)" in the calling thread's error
+// buffer and returns the status unchanged (0 leaves the buffer untouched).
+int hip_status(hipError_t status, const char* operation);
+int blas_status(hipblasStatus_t status, const char* operation);
+int fail(int code, const char* fmt, ...);
+
+// Status of the most recent launch on this thread.
+inline int launch_status() { return hip_status(hipGetLastError(), "HIP kernel launch"); }
+
+inline bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; }
+
+}  // namespace nvr
+
+#define NVR_HIP(call)                                                  \
+    do {                                                               \
+        int nvr_error_ = ::nvr::hip_status((call), #call);             \
+        if (nvr_error_) return nvr_error_;                             \
+    } while (0)
+#define NVR_BLAS(call)                                                 \
+    do {                                                               \
+        int nvr_error_ = ::nvr::blas_status((call), #call);            \
+        if (nvr_error_) return nvr_error_;                             \
+    } while (0)
+#define NVR_ACTIVATE(c) NVR_HIP(hipSetDevice((c)->device))

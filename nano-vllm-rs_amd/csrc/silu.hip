@@ -1,0 +1,76 @@
+// SiLU-gate-mul (nv_silu).
+//
+// Semantics: kernels/kernels.cu:356-365 of nano-vllm-rs. packed is
+// [rows, 2, intermediate] (gate half, then up half, per token):
+//   out[r,i] = bf16( (g / (1 + exp(-g))) * u ),  g = gate[r,i], u = up[r,i]
+// with a single rounding at the store.
+//
+// Numerics: exp uses the hardware base-2 exponential (v_exp_f32 on -g*log2 e)
+// and the division uses v_rcp_f32, which keeps the fp32 result within a few
+// ulp of the correctly rounded expression and so the bf16 output within one
+// bf16 ulp. When 1 + exp(-g) >= 2^126 the quotient is subnormal, where the
+// reciprocal would flush; those lanes take the IEEE division instead.
+//
+// Layout: grid = rows x ceil(intermediate/8 / 256) blocks; a block owns 256
+// 16-byte chunks of one row, so the row index is one scalar division per block.
+#include "../../include/nano_hip.h"
+#include "nvr_device.h"
+#include "nvr_internal.h"
+
+namespace {
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896340736f);
+    const float d = 1.0f + e;
+    const float act = d < 0x1.0p126f ? g * __builtin_amdgcn_rcpf(d) : g / d;
+    return act * u;
+}
+
+__global__ __launch_bounds__(256) void silu16(const uint16_t* __restrict__ packed, uint16_t* __restrict__ out,
+                                              int intermediate, int blocks_per_row) {
+    const int row = blockIdx.x / blocks_per_row;
+    const int part = blockIdx.x - row * blocks_per_row;
+    const int chunk = part * 256 + threadIdx.x;
+    const int chunks = intermediate / 8;
+    if (chunk >= chunks) return;
+    const int64_t gate_base = int64_t(row) * 2 * intermediate + 8 * chunk;
+    const uint4 gw = *reinterpret_cast<const uint4*>(packed + gate_base);
+    const uint4 uw = *reinterpret_cast<const uint4*>(packed + gate_base + intermediate);
+    float g[8], u[8], o[8];
+    nvr::unpack8(gw, g);
+    nvr::unpack8(uw, u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = silu_mul(g[i], u[i]);
+    *reinterpret_cast<uint4*>(out + int64_t(row) * intermediate + 8 * chunk) = nvr::pack8(o);
+}
+
+__global__ __launch_bounds__(256) void silu_generic(const uint16_t* __restrict__ packed, uint16_t* __restrict__ out,
+                                                    int rows, int intermediate) {
+    const int64_t total = int64_t(rows) * intermediate;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t r = i / intermediate, col = i - r * intermediate;
+        const int64_t base = r * 2 * intermediate + col;
+        out[i] = nvr::f32_to_bf16(silu_mul(nvr::bf16_to_f32(packed[base]), nvr::bf16_to_f32(packed[base + intermediate])));
+    }
+}
+
+}  // namespace
+
+extern "C" int nv_silu(nv_context* c, const void* packed, void* out, int rows, int intermediate) {
+    NVR_ACTIVATE(c);
+    if (rows <= 0 || intermediate <= 0) return nvr::fail(-2, "silu: dimensions must be positive");
+    auto in16 = static_cast<const uint16_t*>(packed);
+    auto out16 = static_cast<uint16_t*>(out);
+    const int chunks = intermediate / 8;
+    const int blocks_per_row = (chunks + 255) / 256;
+    const int64_t grid = int64_t(rows) * blocks_per_row;
+    if (intermediate % 8 == 0 && nvr::aligned(packed, 16) && nvr::aligned(out, 16) && grid <= 0x7fffffff) {
+        hipLaunchKernelGGL(silu16, dim3(unsigned(grid)), dim3(256), 0, c->stream, in16, out16, intermediate,
+                           blocks_per_row);
+    } else {
+        const int64_t want = (int64_t(rows) * intermediate + 255) / 256;
+        const unsigned g = unsigned(want > 65535 ? 65535 : want);
+        hipLaunchKernelGGL(silu_generic, dim3(g), dim3(256), 0, c->stream, in16, out16, rows, intermediate);
+    }
+    return nvr::launch_status();
+}

@@ -1,0 +1,344 @@
+"""HIP kernels vs the CPU oracle, through the nv_* C ABI.
+
+Seeded synthetic inputs at the workload shapes (Qwen3-0.6B: hidden 1024,
+intermediate 3072, 16 q heads, 8 kv heads, head dim 128, vocab 151936) plus
+ragged/misaligned/out-of-range edge cases. Bars:
+  - copies, indices, residuals, q/k norm + RoPE, RMSNorm: bit-exact
+    (the kernels keep the oracle's summation order and fp32 rounding points);
+  - SiLU: within 1 bf16 ulp (hardware exp/reciprocal vs the C library).
+"""
+import numpy as np
+import pytest
+
+import nvr
+import oracle as ora
+from helpers import assert_bits_equal, bf16_of, bf16_ulp_diff, f32_of, unique_slots
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+THETA = 1e6
+
+
+def up(gpu, arr):
+    return gpu.upload_array(np.ascontiguousarray(arr))
+
+
+def down(buf, dtype, shape):
+    return buf.download(dtype, int(np.prod(shape))).reshape(shape)
+
+
+def misaligned(gpu, arr):
+    """Upload `arr` at a 2-byte offset so only the generic kernels apply."""
+    arr = np.ascontiguousarray(arr)
+    raw = gpu.alloc(arr.nbytes + 16)
+    view = raw.slice(2, arr.nbytes)
+    view.upload(arr)
+    return view
+
+
+# ------------------------------------------------------------------ norms ----
+def test_rms_small_rows(gpu):
+    """8 tokens x 1024 (RMSNorm-only workload)."""
+    x = ora.normal_bf16((8, 1024), 0)
+    w = ora.normal_bf16(1024, 1, 1.0, 0.02)
+    out = gpu.alloc(8 * 1024 * 2)
+    gpu.rms_norm(up(gpu, x), up(gpu, w), out, 8, 1024, EPS)
+    got = down(out, np.uint16, (8, 1024))
+    assert_bits_equal(got, ora.rms(x, w, 8, 1024, EPS))
+
+
+def test_add_rms_8192x1024(gpu):
+    rows, hidden = 8192, 1024
+    x = ora.normal_bf16((rows, hidden), 2)
+    res = ora.normal_bf16((rows, hidden), 3)
+    w = ora.normal_bf16(hidden, 4, 1.0, 0.02)
+    rb = up(gpu, res)
+    out = gpu.alloc(rows * hidden * 2)
+    gpu.add_rms_norm(up(gpu, x), rb, up(gpu, w), out, rows, hidden, EPS)
+    want_res, want_out = ora.add_rms(x, res, w, rows, hidden, EPS, threads=8)
+    assert_bits_equal(down(rb, np.uint16, (rows, hidden)), want_res)
+    assert_bits_equal(down(out, np.uint16, (rows, hidden)), want_out)
+
+
+@pytest.mark.parametrize("rows,hidden", [(7, 256), (33, 2048), (5, 4096), (3, 5120), (9, 1536)])
+def test_rms_other_hidden_sizes(gpu, rows, hidden):
+    x = ora.normal_bf16((rows, hidden), 5 + hidden)
+    res = ora.normal_bf16((rows, hidden), 6 + hidden)
+    w = ora.normal_bf16(hidden, 7, 1.0, 0.02)
+    out = gpu.alloc(rows * hidden * 2)
+    gpu.rms_norm(up(gpu, x), up(gpu, w), out, rows, hidden, EPS)
+    assert_bits_equal(down(out, np.uint16, (rows, hidden)), ora.rms(x, w, rows, hidden, EPS))
+    rb = up(gpu, res)
+    gpu.add_rms_norm(up(gpu, x), rb, up(gpu, w), out, rows, hidden, EPS)
+    want_res, want_out = ora.add_rms(x, res, w, rows, hidden, EPS)
+    assert_bits_equal(down(rb, np.uint16, (rows, hidden)), want_res)
+    assert_bits_equal(down(out, np.uint16, (rows, hidden)), want_out)
+
+
+@pytest.mark.parametrize("hidden", [1000, 1024, 1, 3])
+def test_rms_generic_path_misaligned(gpu, hidden):
+    rows = 5
+    x = ora.normal_bf16((rows, hidden), 8)
+    res = ora.normal_bf16((rows, hidden), 9)
+    w = ora.normal_bf16(hidden, 10, 1.0, 0.02)
+    out = misaligned(gpu, np.zeros((rows, hidden), np.uint16))
+    gpu.rms_norm(misaligned(gpu, x), misaligned(gpu, w), out, rows, hidden, EPS)
+    assert_bits_equal(down(out, np.uint16, (rows, hidden)), ora.rms(x, w, rows, hidden, EPS))
+    rb = misaligned(gpu, res)
+    gpu.add_rms_norm(misaligned(gpu, x), rb, misaligned(gpu, w), out, rows, hidden, EPS)
+    want_res, want_out = ora.add_rms(x, res, w, rows, hidden, EPS)
+    assert_bits_equal(down(rb, np.uint16, (rows, hidden)), want_res)
+    assert_bits_equal(down(out, np.uint16, (rows, hidden)), want_out)
+
+
+# ------------------------------------------------------------------- RoPE ----
+def test_rope_table_bit_exact(gpu):
+    table = gpu.alloc(4096 * 128 * 4)
+    gpu.rope_cache(table, 4096, 128, THETA)
+    assert_bits_equal(down(table, np.float32, (4096, 128)), ora.rope_cache(4096, 128, THETA, threads=8))
+
+
+def _rope_case(gpu, rows, qh, kvh, dim, bs, blocks, seed, positions, slots, cached=True, align=True):
+    heads = qh + 2 * kvh
+    qkv = ora.normal_bf16((rows, heads, dim), seed)
+    qw = ora.normal_bf16(dim, seed + 1, 1.0, 0.02)
+    kw = ora.normal_bf16(dim, seed + 2, 1.0, 0.02)
+    cache0 = ora.normal_bf16((blocks, bs, kvh, dim), seed + 3)  # stale contents must survive skipped slots
+    put = up if align else misaligned
+    kcb, vcb = put(gpu, cache0), put(gpu, cache0)
+    qout = put(gpu, np.zeros((rows, qh, dim), np.uint16))
+    args = (put(gpu, qkv), put(gpu, qw), put(gpu, kw), up(gpu, positions), up(gpu, slots), qout, kcb, vcb, rows, qh,
+            kvh, dim, bs, blocks, EPS)
+    if cached:
+        tb = gpu.alloc(4096 * dim * 4)
+        gpu.rope_cache(tb, 4096, dim, THETA)
+        table = down(tb, np.float32, (4096, dim))
+        gpu.qkv_rope_cached(*args, tb, 4096)
+        want = ora.qkv_rope(qkv, qw, kw, positions, slots, cache0, cache0, rows, qh, kvh, dim, bs, blocks, EPS,
+                            table=table, max_positions=4096, threads=8)
+    else:
+        gpu.qkv_rope(*args, THETA)
+        want = ora.qkv_rope(qkv, qw, kw, positions, slots, cache0, cache0, rows, qh, kvh, dim, bs, blocks, EPS,
+                            theta=THETA, threads=8)
+    got = (down(qout, np.uint16, (rows, qh, dim)), down(kcb, np.uint16, cache0.shape),
+           down(vcb, np.uint16, cache0.shape))
+    for name, g, w in zip(("q", "k cache", "v cache"), got, want):
+        assert_bits_equal(g, w, name)
+
+
+def test_qkv_rope_cached_2048_tokens(gpu):
+    rows, bs = 2048, 256
+    blocks = rows // bs
+    pos = np.random.default_rng(11).integers(0, 4096, rows).astype(np.int32)
+    _rope_case(gpu, rows, 16, 8, 128, bs, blocks, 40, pos, unique_slots(rows, bs, blocks, 12))
+
+
+def test_qkv_rope_cached_8192_tokens(gpu):
+    rows, bs = 8192, 256
+    blocks = rows // bs
+    pos = np.random.default_rng(13).integers(0, 4096, rows).astype(np.int32)
+    _rope_case(gpu, rows, 16, 8, 128, bs, blocks, 50, pos, unique_slots(rows, bs, blocks, 14))
+
+
+def test_qkv_rope_guards(gpu):
+    """Positions outside the table rotate by 0; slots outside the cache are skipped."""
+    rows, bs, blocks = 12, 4, 4
+    pos = np.array([0, 1, -1, 4096, 5000, 4095, 2**31 - 1, -2**31, 7, 8, 9, 10], np.int32)
+    slots = np.array([0, 15, -1, 16, 3, 100, 5, 6, -7, 2**31 - 1, 9, 10], np.int32)
+    _rope_case(gpu, rows, 16, 8, 128, bs, blocks, 60, pos, slots)
+
+
+@pytest.mark.parametrize("dim,qh,kvh,align", [(64, 4, 2, True), (96, 6, 3, True), (128, 16, 8, False),
+                                              (256, 2, 1, True), (2, 2, 2, True)])
+def test_qkv_rope_generic_shapes(gpu, dim, qh, kvh, align):
+    rows, bs, blocks = 17, 4, 5
+    pos = np.random.default_rng(dim).integers(0, 4096, rows).astype(np.int32)
+    _rope_case(gpu, rows, qh, kvh, dim, bs, blocks, 70 + dim, pos, unique_slots(rows, bs, blocks, dim), align=align)
+
+
+def test_qkv_rope_direct_matches_oracle(gpu):
+    rows, bs, blocks = 64, 16, 4
+    pos = np.random.default_rng(15).integers(0, 4096, rows).astype(np.int32)
+    _rope_case(gpu, rows, 16, 8, 128, bs, blocks, 80, pos, unique_slots(rows, bs, blocks, 16), cached=False)
+
+
+# ------------------------------------------------------------------- SiLU ----
+def test_silu_8192x3072(gpu):
+    rows, inter = 8192, 3072
+    gu = ora.normal_bf16((rows, 2, inter), 90, 0.0, 2.0)
+    out = gpu.alloc(rows * inter * 2)
+    gpu.silu_mul(up(gpu, gu), out, rows, inter)
+    got = down(out, np.uint16, (rows, inter))
+    want = ora.silu(gu, rows, inter, threads=8)
+    d = bf16_ulp_diff(got, want)
+    assert d.max() <= 1, f"max {d.max()} ulp"
+    assert np.mean(d == 0) > 0.999
+
+
+def test_silu_edges_and_generic(gpu):
+    g = np.array([-1e4, -100.0, -88.5, -87.0, -20.0, -0.0, 0.0, 1e-30, 3.0, 88.0, 1e4, np.inf, -np.inf, np.nan, 1.0,
+                  -1.0], np.float32)
+    u = np.array([1.0, 2.0, -3.0, 0.5, 1.0, 1.0, -1.0, 1.0, np.inf, 2.0, -1.0, 1.0, 1.0, 1.0, np.nan, 0.0],
+                 np.float32)
+    gu = np.stack([bf16_of(g), bf16_of(u)])[None]  # [1, 2, 16]
+    out = gpu.alloc(32)
+    gpu.silu_mul(up(gpu, gu), out, 1, 16)
+    got = down(out, np.uint16, (1, 16))
+    assert bf16_ulp_diff(got, ora.silu(gu, 1, 16)).max() <= 1
+    rows, inter = 7, 1001
+    gu2 = ora.normal_bf16((rows, 2, inter), 91, 0.0, 2.0)
+    out2 = misaligned(gpu, np.zeros((rows, inter), np.uint16))
+    gpu.silu_mul(misaligned(gpu, gu2), out2, rows, inter)
+    assert bf16_ulp_diff(down(out2, np.uint16, (rows, inter)), ora.silu(gu2, rows, inter)).max() <= 1
+
+
+# ------------------------------------------------------------------ copies ---
+def test_embedding_16384_tokens(gpu):
+    vocab, hidden, rows = 151936, 1024, 16384
+    table = ora.normal_bf16((vocab, hidden), 100, 0.0, 0.02)
+    tokens = np.random.default_rng(101).integers(0, vocab, rows).astype(np.int32)
+    tokens[[5, 77, 9000]] = [-1, vocab, 2**31 - 1]  # out of range -> +0 rows
+    out = gpu.alloc(rows * hidden * 2)
+    gpu.embedding(up(gpu, tokens), up(gpu, table), out, rows, hidden, vocab)
+    assert_bits_equal(down(out, np.uint16, (rows, hidden)), ora.embedding(tokens, table, rows, hidden, vocab))
+
+
+@pytest.mark.parametrize("hidden,align", [(1, True), (12, True), (1000, False), (2048, True)])
+def test_gather_shapes(gpu, hidden, align):
+    input_rows, rows = 50, 23
+    x = ora.normal_bf16((input_rows, hidden), 110 + hidden)
+    idx = np.random.default_rng(hidden).integers(-3, input_rows + 3, rows).astype(np.int32)
+    put = up if align else misaligned
+    out = put(gpu, np.zeros((rows, hidden), np.uint16))
+    gpu.gather(put(gpu, x), up(gpu, idx), out, rows, hidden, input_rows)
+    assert_bits_equal(down(out, np.uint16, (rows, hidden)), ora.gather(x, idx, rows, hidden, input_rows))
+
+
+def test_kv_write_16384_tokens(gpu):
+    rows, kvh, dim, bs, blocks = 16384, 8, 128, 256, 64
+    k = ora.normal_bf16((rows, kvh, dim), 120)
+    v = ora.normal_bf16((rows, kvh, dim), 121)
+    slots = unique_slots(rows, bs, blocks, 122)
+    slots[[3, 4000]] = [-1, bs * blocks]  # skipped rows
+    cache0 = np.zeros((blocks, bs, kvh, dim), np.uint16)
+    kc, vc = up(gpu, cache0), up(gpu, cache0)
+    gpu.kv_write(up(gpu, k), up(gpu, v), up(gpu, slots), kc, vc, rows, kvh, dim, bs, blocks)
+    want_k, want_v = ora.kv_write(k, v, slots, cache0, cache0, rows, kvh, dim, bs, blocks)
+    assert_bits_equal(down(kc, np.uint16, cache0.shape), want_k)
+    assert_bits_equal(down(vc, np.uint16, cache0.shape), want_v)
+
+
+def test_kv_write_generic(gpu):
+    rows, kvh, dim, bs, blocks = 9, 3, 6, 2, 8
+    k = ora.normal_bf16((rows, kvh, dim), 123)
+    v = ora.normal_bf16((rows, kvh, dim), 124)
+    slots = unique_slots(rows, bs, blocks, 125)
+    cache0 = np.zeros((blocks, bs, kvh, dim), np.uint16)
+    kc, vc = misaligned(gpu, cache0), misaligned(gpu, cache0)
+    gpu.kv_write(misaligned(gpu, k), misaligned(gpu, v), up(gpu, slots), kc, vc, rows, kvh, dim, bs, blocks)
+    want_k, want_v = ora.kv_write(k, v, slots, cache0, cache0, rows, kvh, dim, bs, blocks)
+    assert_bits_equal(down(kc, np.uint16, cache0.shape), want_k)
+    assert_bits_equal(down(vc, np.uint16, cache0.shape), want_v)
+
+
+# ---------------------------------------------------------------- sampling ---
+def sampling_batch(batch=256, vocab=151936, seed=130):
+    """Logits ~N(0,3); round(0.01*batch) rows get +20 at a random index; first half
+    greedy, second half T=0.6; seeds from src/runtime.rs:780-790."""
+    logits = ora.normal_bf16((batch, vocab), seed, 0.0, 3.0)
+    rng = np.random.default_rng(seed + 1)
+    spiked = rng.choice(batch, size=max(1, round(0.01 * batch)), replace=False)
+    for r in spiked:
+        i = int(rng.integers(0, vocab))
+        logits[r, i] = bf16_of(f32_of(logits[r, i]) + np.float32(20.0))
+    temps = np.where(np.arange(batch) < batch // 2, 0.0, 0.6).astype(np.float32)
+    seeds = np.array([ora.sampling_seed(0, r, r % 32) for r in range(batch)], np.uint64)
+    return logits, temps, seeds
+
+
+def _run_sampler(gpu, logits, temps, seeds, batch, vocab, parallel=True, align=True):
+    put = up if align else misaligned
+    lb, tb, sb = put(gpu, logits), up(gpu, temps), up(gpu, seeds)
+    out = gpu.alloc(batch * 4)
+    if parallel:
+        parts = -(-vocab // 2048)
+        ps, pi = gpu.alloc(batch * parts * 4), gpu.alloc(batch * parts * 4)
+        gpu.sample_parallel(lb, tb, sb, out, ps, pi, batch, vocab)
+    else:
+        gpu.sample(lb, tb, sb, out, batch, vocab)
+    return out.download(np.int32, batch)
+
+
+def test_sampling_256x151936(gpu):
+    batch, vocab = 256, 151936
+    logits, temps, seeds = sampling_batch(batch, vocab)
+    want = ora.sample(logits, temps, seeds, batch, vocab, threads=8)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab), want)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab, parallel=False), want)
+
+
+@pytest.mark.parametrize("batch", [1, 3, 8, 64])
+def test_sampling_small_batches(gpu, batch):
+    vocab = 151936
+    logits, temps, seeds = sampling_batch(batch, vocab, seed=140 + batch)
+    temps[:] = np.where(np.arange(batch) % 2 == 0, 0.0, 1.3)
+    want = ora.sample(logits, temps, seeds, batch, vocab, threads=8)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab), want)
+
+
+@pytest.mark.parametrize("vocab,align", [(5, True), (2048, True), (2049, True), (10001, False), (151936, False)])
+def test_sampling_ragged_vocab(gpu, vocab, align):
+    batch = 4
+    logits = ora.normal_bf16((batch, vocab), 150 + vocab, 0.0, 3.0)
+    temps = np.array([0.0, 0.6, 1.0, -1.0], np.float32)
+    seeds = np.array([42, 43, 44, 45], np.uint64)
+    want = ora.sample(logits, temps, seeds, batch, vocab)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab, align=align), want)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab, parallel=False, align=align), want)
+
+
+def test_sampling_special_values(gpu):
+    vocab = 4096
+    rows = np.stack([
+        bf16_of(np.full(vocab, np.nan)),
+        bf16_of(np.full(vocab, -np.inf)),
+        bf16_of(np.where(np.arange(vocab) == 3000, np.inf, np.nan)),
+        bf16_of(np.r_[np.full(vocab - 1, -1.0), 5.0]),
+        bf16_of(np.where(np.arange(vocab) % 2048 == 2047, 9.0, 0.0)),
+    ])
+    for t in (0.0, 0.8):
+        temps = np.full(5, t, np.float32)
+        seeds = np.arange(5, dtype=np.uint64)
+        want = ora.sample(rows, temps, seeds, 5, vocab)
+        assert_bits_equal(_run_sampler(gpu, rows, temps, seeds, 5, vocab), want)
+        assert_bits_equal(_run_sampler(gpu, rows, temps, seeds, 5, vocab, parallel=False), want)
+
+
+def test_sampling_reference_golden_vectors(gpu):
+    import os
+
+    data = np.load(os.path.join(os.path.dirname(__file__), "golden", "reference_logits.npz"))
+    logits, expected = data["logits_bf16"], data["expected_greedy"]
+    b, v = logits.shape
+    temps, seeds = np.zeros(b, np.float32), np.zeros(b, np.uint64)
+    assert _run_sampler(gpu, logits, temps, seeds, b, v).tolist() == expected.tolist()
+    assert _run_sampler(gpu, logits, temps, seeds, b, v, parallel=False).tolist() == expected.tolist()
+
+
+# ------------------------------------------------------------------- GEMM ----
+def test_gemm_known_answer_and_random(gpu):
+    # src/gpu.rs:1290-1298: X = [[1,2,3],[4,5,6]], W = [[1,0,1],[0,1,0]] -> [[4,2],[10,5]].
+    x = up(gpu, bf16_of([1, 2, 3, 4, 5, 6]))
+    w = up(gpu, bf16_of([1, 0, 1, 0, 1, 0]))
+    y = gpu.alloc(8)
+    gpu.gemm(x, w, y, 2, 2, 3)
+    assert f32_of(y.download(np.uint16, 4)).tolist() == [4.0, 2.0, 10.0, 5.0]
+    m, n, k = 64, 96, 256
+    xa = ora.normal_bf16((m, k), 160)
+    wa = ora.normal_bf16((n, k), 161)
+    yb = gpu.alloc(m * n * 2)
+    gpu.gemm(up(gpu, xa), up(gpu, wa), yb, m, n, k)
+    got = f32_of(down(yb, np.uint16, (m, n))).astype(np.float64)
+    want = f32_of(xa).astype(np.float64) @ f32_of(wa).astype(np.float64).T
+    assert np.max(np.abs(got - want) / (np.abs(want) + 1.0)) < 1e-2
