@@ -1,0 +1,462 @@
+#!/usr/bin/env python3
+"""Benchmark of the nano-vllm-rs fused per-layer kernels on one MI355X.
+
+Step (the `value` workload): the fused, non-GEMM kernels of one Qwen3-0.6B
+forward pass over T = 8192 prompt tokens, in the reference's order
+(src/model.rs:649-789):
+
+    embedding(tokens -> residual)
+    layer 0: rms(residual -> normed)            layers 1..27: add_rms(mlp_out[l-1], residual -> normed)
+             qkv_rope_cached(qkv[l] -> query, kcache[l], vcache[l])
+             add_rms(attn_out[l], residual -> normed)
+             silu(gate_up[l] -> act)
+    add_rms(mlp_out[27], residual -> normed)     (final norm)
+
+The GEMM/attention outputs that feed these kernels (qkv[l], attn_out[l],
+gate_up[l], mlp_out[l]) are synthetic bf16 tensors, one per layer, resident
+in HBM before timing starts. The step is captured once as a HIP graph and
+replayed; `value` is tokens per second of that step.
+
+Per-kernel lines reproduce the kernel workloads (RMSNorm 8x1024, q/k norm +
+RoPE at 2048 and 8192 tokens, add-RMSNorm 8192x1024, SiLU 8192x6144, embedding
+and KV write at 16384 tokens, sampling 256x151936). Each is launched over
+several distinct buffer sets totalling more than 512 MB so that no launch finds
+its data in the 256 MB Infinity Cache; time is HIP events on the library's
+stream around the whole loop, divided by the launch count.
+
+The CPU baseline runs the oracle's multithreaded C restatement of the same
+step (all 28 layers, T = 8192) on the host cores.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-kernels]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "nano-vllm-rs_amd"))
+
+import nvr  # noqa: E402
+
+METRIC = "achieved HBM GB/s and % roofline per fused kernel; tokens/s at T=8192, 1 MI355X"
+HBM_PEAK_GBS = 8000.0
+
+# Qwen3-0.6B shapes (src/model.rs:1407-1411).
+H, I, QH, KVH, D, V, LAYERS = 1024, 3072, 16, 8, 128, 151936, 28
+HEADS = QH + 2 * KVH
+EPS, THETA, MAX_POS, BS = 1e-6, 1e6, 4096, 256
+MALL_DEFEAT_BYTES = 640 << 20
+
+
+# ------------------------------------------------------------ HIP plumbing --
+class Hip:
+    """Events and device copies from the HIP runtime the library already loaded."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        vp = ctypes.c_void_p
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(vp)]
+        self.lib.hipEventRecord.argtypes = [vp, vp]
+        self.lib.hipEventSynchronize.argtypes = [vp]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        self.lib.hipEventDestroy.argtypes = [vp]
+        self.lib.hipMemcpyAsync.argtypes = [vp, vp, ctypes.c_size_t, ctypes.c_int, vp]
+        self.lib.hipStreamSynchronize.argtypes = [vp]
+        self.lib.hipDeviceSynchronize.argtypes = []
+
+    def check(self, code, what):
+        if code != 0:
+            raise RuntimeError(f"{what} failed with HIP status {code}")
+
+    def event(self):
+        e = ctypes.c_void_p()
+        self.check(self.lib.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e
+
+    def record(self, e, stream):
+        self.check(self.lib.hipEventRecord(e, stream), "hipEventRecord")
+
+    def elapsed_ms(self, a, b):
+        self.check(self.lib.hipEventSynchronize(b), "hipEventSynchronize")
+        ms = ctypes.c_float()
+        self.check(self.lib.hipEventElapsedTime(ctypes.byref(ms), a, b), "hipEventElapsedTime")
+        return float(ms.value)
+
+    def copy_d2d(self, dst, src, nbytes, stream):
+        self.check(self.lib.hipMemcpyAsync(dst, src, nbytes, 3, stream), "hipMemcpyAsync")
+
+    def device_sync(self):
+        self.check(self.lib.hipDeviceSynchronize(), "hipDeviceSynchronize")
+
+
+class Filler:
+    """Fills device buffers with seeded bf16 normals: one host-generated pool per
+    distribution is uploaded once, then tiled with device-to-device copies."""
+
+    POOL = 16 << 20  # elements (32 MiB of bf16)
+
+    def __init__(self, gpu: nvr.Gpu, hip: Hip):
+        self.gpu, self.hip, self.pools = gpu, hip, {}
+        self.stream = gpu.stream()
+
+    def pool(self, mean, std):
+        key = (mean, std)
+        if key not in self.pools:
+            rng = np.random.default_rng(abs(hash(key)) % (2**32))
+            vals = (mean + std * rng.standard_normal(self.POOL, dtype=np.float32)).astype(np.float32)
+            self.pools[key] = self.gpu.upload_array(nvr.bf16_bits(vals))
+        return self.pools[key]
+
+    def normal(self, nbytes, mean=0.0, std=1.0):
+        buf = self.gpu.alloc(nbytes)
+        src = self.pool(mean, std)
+        off = 0
+        # Start each buffer at a different pool offset so tiles are not identical.
+        shift = int(np.random.default_rng(nbytes ^ int(std * 1000)).integers(0, src.bytes // 2)) & ~15
+        while off < nbytes:
+            n = min(src.bytes - shift, nbytes - off)
+            self.hip.copy_d2d(buf.ptr + off, src.ptr + shift, n, self.stream)
+            off += n
+            shift = 0
+        return buf
+
+    def ints(self, values: np.ndarray):
+        return self.gpu.upload_array(np.ascontiguousarray(values, dtype=np.int32))
+
+
+# ----------------------------------------------------- algorithmic bytes --
+def bytes_rms(rows, hidden):
+    return 2 * rows * hidden * 2 + hidden * 2
+
+
+def bytes_add_rms(rows, hidden):
+    return 4 * rows * hidden * 2 + hidden * 2
+
+
+def bytes_qkv_rope(rows, distinct_positions):
+    return rows * HEADS * D * 2 * 2 + rows * 8 + 2 * D * 2 + distinct_positions * D * 4
+
+
+def bytes_silu(rows, inter):
+    return rows * 3 * inter * 2
+
+
+def bytes_embedding(rows, hidden):
+    return rows * 4 + 2 * rows * hidden * 2
+
+
+def bytes_kv_write(rows):
+    return rows * 4 + 2 * 2 * rows * KVH * D * 2
+
+
+def bytes_sampling(batch, vocab):
+    return batch * vocab * 2 + batch * (4 + 8 + 4)
+
+
+# ------------------------------------------------------------- the step ----
+class Chain:
+    def __init__(self, gpu: nvr.Gpu, fill: Filler, tokens: int, layers: int, seed: int = 0):
+        self.gpu, self.T, self.L = gpu, tokens, layers
+        T = tokens
+        rng = np.random.default_rng(seed)
+        self.blocks = -(-T // BS)
+        self.tok = fill.ints(rng.integers(0, V, T))
+        self.table = fill.normal(V * H * 2, 0.0, 0.02)
+        self.residual = gpu.alloc(T * H * 2)
+        self.normed = gpu.alloc(T * H * 2)
+        self.query = gpu.alloc(T * QH * D * 2)
+        self.act = gpu.alloc(T * I * 2)
+        # Prefill batch of sequences of MAX_POS tokens: positions restart per
+        # sequence; slots come from a random permutation of cache blocks.
+        pos = (np.arange(T) % MAX_POS).astype(np.int32)
+        perm = rng.permutation(self.blocks)
+        slots = (perm[np.arange(T) // BS] * BS + np.arange(T) % BS).astype(np.int32)
+        self.distinct_positions = int(len(np.unique(pos)))
+        self.pos, self.slots = fill.ints(pos), fill.ints(slots)
+        self.rope = gpu.alloc(MAX_POS * D * 4)
+        gpu.rope_cache(self.rope, MAX_POS, D, THETA)
+        self.final_norm = fill.normal(H * 2, 1.0, 0.02)
+        self.layers = []
+        for _ in range(layers):
+            self.layers.append(dict(
+                in_norm=fill.normal(H * 2, 1.0, 0.02), post_norm=fill.normal(H * 2, 1.0, 0.02),
+                q_norm=fill.normal(D * 2, 1.0, 0.02), k_norm=fill.normal(D * 2, 1.0, 0.02),
+                qkv=fill.normal(T * HEADS * D * 2), attn_out=fill.normal(T * H * 2),
+                gate_up=fill.normal(T * 2 * I * 2, 0.0, 2.0), mlp_out=fill.normal(T * H * 2),
+                kc=gpu.alloc(self.blocks * BS * KVH * D * 2), vc=gpu.alloc(self.blocks * BS * KVH * D * 2)))
+
+    def step(self):
+        g, T = self.gpu, self.T
+        g.embedding(self.tok, self.table, self.residual, T, H, V)
+        for i, l in enumerate(self.layers):
+            if i == 0:
+                g.rms_norm(self.residual, l["in_norm"], self.normed, T, H, EPS)
+            else:
+                g.add_rms_norm(self.layers[i - 1]["mlp_out"], self.residual, l["in_norm"], self.normed, T, H, EPS)
+            g.qkv_rope_cached(l["qkv"], l["q_norm"], l["k_norm"], self.pos, self.slots, self.query, l["kc"], l["vc"],
+                              T, QH, KVH, D, BS, self.blocks, EPS, self.rope, MAX_POS)
+            g.add_rms_norm(l["attn_out"], self.residual, l["post_norm"], self.normed, T, H, EPS)
+            g.silu_mul(l["gate_up"], self.act, T, I)
+        g.add_rms_norm(self.layers[-1]["mlp_out"], self.residual, self.final_norm, self.normed, T, H, EPS)
+
+    def bytes(self):
+        T, L = self.T, self.L
+        return (bytes_embedding(T, H) + bytes_rms(T, H) + (2 * L - 1) * bytes_add_rms(T, H) + bytes_add_rms(T, H)
+                + L * bytes_qkv_rope(T, self.distinct_positions) + L * bytes_silu(T, I))
+
+    def launches(self):
+        return {"embedding": 1, "rms": 1, "add_rms": 2 * self.L, "qkv_rope_cached": self.L, "silu": self.L}
+
+
+def time_graph(gpu, hip, graph, reps, warmup):
+    stream = gpu.stream()
+    for _ in range(warmup):
+        graph.replay()
+    gpu.sync()
+    hip.device_sync()
+    a, b = hip.event(), hip.event()
+    hip.record(a, stream)
+    for _ in range(reps):
+        graph.replay()
+    hip.record(b, stream)
+    ms = hip.elapsed_ms(a, b)
+    gpu.sync()
+    hip.device_sync()
+    return ms / reps
+
+
+# ------------------------------------------------------ per-kernel loops ---
+def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain):
+    """Yields (name, workload, launch closures over rotating sets, bytes per launch, rows per launch)."""
+    cases = []
+
+    def sets_for(per_set_bytes):
+        return max(3, -(-MALL_DEFEAT_BYTES // per_set_bytes))
+
+    # RMSNorm 8 x 1024 (latency-bound decode shape).
+    n = 64
+    xs = [fill.normal(8 * H * 2) for _ in range(n)]
+    w = fill.normal(H * 2, 1.0, 0.02)
+    outs = [gpu.alloc(8 * H * 2) for _ in range(n)]
+    cases.append(("rms_8x1024", "RMSNorm x[8,1024]",
+                  [lambda i=i: gpu.rms_norm(xs[i], w, outs[i], 8, H, EPS) for i in range(n)], bytes_rms(8, H), 8))
+
+    # add-RMSNorm 8192 x 1024.
+    T = 8192
+    per = 3 * T * H * 2
+    s = sets_for(per)
+    ax = [fill.normal(T * H * 2) for _ in range(s)]
+    ar = [fill.normal(T * H * 2) for _ in range(s)]
+    ao = [gpu.alloc(T * H * 2) for _ in range(s)]
+    cases.append(("add_rms_8192x1024", "residual add + RMSNorm [8192,1024]",
+                  [lambda i=i, T=T: gpu.add_rms_norm(ax[i], ar[i], w, ao[i], T, H, EPS) for i in range(s)],
+                  bytes_add_rms(T, H), T))
+
+    # SiLU 8192 x 6144 -> 8192 x 3072.
+    per = 3 * T * I * 2
+    s = sets_for(per)
+    gus = [fill.normal(T * 2 * I * 2, 0.0, 2.0) for _ in range(s)]
+    acts = [gpu.alloc(T * I * 2) for _ in range(s)]
+    cases.append(("silu_8192x6144", "SiLU(gate)*up [8192,6144] -> [8192,3072]",
+                  [lambda i=i, T=T: gpu.silu_mul(gus[i], acts[i], T, I) for i in range(s)], bytes_silu(T, I), T))
+
+    # q/k norm + RoPE + KV write at 2048 and 8192 tokens, uniform random positions.
+    for T in (2048, 8192):
+        rng = np.random.default_rng(T)
+        pos = rng.integers(0, MAX_POS, T).astype(np.int32)
+        blocks = T // BS
+        perm = rng.permutation(blocks)
+        slots = (perm[np.arange(T) // BS] * BS + np.arange(T) % BS).astype(np.int32)
+        pb, sb = fill.ints(pos), fill.ints(slots)
+        per = T * HEADS * D * 2 * 2
+        s = sets_for(per)
+        qkvs = [fill.normal(T * HEADS * D * 2) for _ in range(s)]
+        qos = [gpu.alloc(T * QH * D * 2) for _ in range(s)]
+        kcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
+        vcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
+        qn, kn = fill.normal(D * 2, 1.0, 0.02), fill.normal(D * 2, 1.0, 0.02)
+        nbytes = bytes_qkv_rope(T, len(np.unique(pos)))
+        cases.append((f"qkv_rope_{T}", f"q/k RMSNorm + NeoX RoPE + KV write, {T} tokens",
+                      [lambda i=i, T=T, pb=pb, sb=sb, blocks=blocks, qkvs=qkvs, qos=qos, kcs=kcs, vcs=vcs, qn=qn,
+                       kn=kn: gpu.qkv_rope_cached(qkvs[i], qn, kn, pb, sb, qos[i], kcs[i], vcs[i], T, QH, KVH, D, BS,
+                                                  blocks, EPS, chain.rope, MAX_POS) for i in range(s)],
+                      nbytes, T))
+
+    # Embedding gather, 16384 tokens from a [151936, 1024] table (three tables).
+    T = 16384
+    tables = [chain.table] + [fill.normal(V * H * 2, 0.0, 0.02) for _ in range(2)]
+    toks = [fill.ints(np.random.default_rng(100 + j).integers(0, V, T)) for j in range(6)]
+    eouts = [gpu.alloc(T * H * 2) for _ in range(6)]
+    cases.append(("embedding_16384", "embedding gather, 16384 tokens, table [151936,1024]",
+                  [lambda j=j, T=T: gpu.embedding(toks[j], tables[j % 3], eouts[j], T, H, V) for j in range(6)],
+                  bytes_embedding(T, H), T))
+
+    # Paged KV write, k/v [16384, 8, 128] into per-layer caches.
+    blocks = T // BS
+    per = 4 * T * KVH * D * 2
+    s = sets_for(per)
+    ks = [fill.normal(T * KVH * D * 2) for _ in range(s)]
+    vs = [fill.normal(T * KVH * D * 2) for _ in range(s)]
+    kcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
+    vcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
+    rng = np.random.default_rng(7)
+    perm = rng.permutation(blocks)
+    sl = fill.ints((perm[np.arange(T) // BS] * BS + np.arange(T) % BS).astype(np.int32))
+    cases.append(("kv_write_16384", "paged KV write k,v [16384,8,128]",
+                  [lambda i=i, T=T, blocks=blocks, ks=ks, vs=vs, kcs=kcs, vcs=vcs: gpu.kv_write(ks[i], vs[i], sl, kcs[i], vcs[i], T, KVH, D, BS, blocks)
+                   for i in range(s)], bytes_kv_write(T), T))
+
+    # Sampling 256 x 151936: rows 0-127 greedy, 128-255 Gumbel at T=0.6.
+    B = 256
+    per = B * V * 2
+    s = sets_for(per)
+    logits = [fill.normal(B * V * 2, 0.0, 3.0) for _ in range(s)]
+    parts = -(-V // 2048)
+    ps, pi = gpu.alloc(B * parts * 4), gpu.alloc(B * parts * 4)
+    out = gpu.alloc(B * 4)
+    seeds = gpu.upload_array(np.array([nvr.sampling_seed(0, r, r % 32) for r in range(B)], np.uint64))
+    mixed = gpu.upload_array(np.where(np.arange(B) < 128, 0.0, 0.6).astype(np.float32))
+    greedy = gpu.upload_array(np.zeros(B, np.float32))
+    gumbel = gpu.upload_array(np.full(B, 0.6, np.float32))
+    for name, temps, label in (("sampling_256x151936", mixed, "128 greedy + 128 Gumbel (T=0.6) rows"),
+                               ("sampling_greedy", greedy, "256 greedy rows"),
+                               ("sampling_gumbel", gumbel, "256 Gumbel rows (T=0.6)")):
+        cases.append((name, f"sampling logits [256,151936], {label}",
+                      [lambda i=i, temps=temps, B=B: gpu.sample_parallel(logits[i], temps, seeds, out, ps, pi, B, V)
+                       for i in range(s)], bytes_sampling(B, V), B))
+    return cases
+
+
+def run_kernel_case(gpu, hip, launches, rounds):
+    """Average launch time (ms) over `rounds` passes through the rotating sets."""
+    graph = gpu.capture(lambda: [f() for f in launches])
+    per_pass_ms = time_graph(gpu, hip, graph, rounds, 2)
+    return per_pass_ms / len(launches)
+
+
+# -------------------------------------------------------------- CPU leg ----
+def cpu_baseline(tokens: int, layers: int, threads: int) -> dict:
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as ora
+
+    T = tokens
+    tok = np.random.default_rng(0).integers(0, V, T).astype(np.int32)
+    table = ora.normal_bf16((V, H), 1, 0.0, 0.02)
+    x_attn = ora.normal_bf16((T, H), 2)
+    x_mlp = ora.normal_bf16((T, H), 3)
+    qkv = ora.normal_bf16((T, HEADS, D), 4)
+    gu = ora.normal_bf16((T, 2, I), 5, 0.0, 2.0)
+    wn = ora.normal_bf16(H, 6, 1.0, 0.02)
+    qn, kn = ora.normal_bf16(D, 7, 1.0, 0.02), ora.normal_bf16(D, 8, 1.0, 0.02)
+    pos = (np.arange(T) % MAX_POS).astype(np.int32)
+    blocks = -(-T // BS)
+    slots = np.arange(T, dtype=np.int32)
+    rope = ora.rope_cache(MAX_POS, D, THETA, threads)
+    kc = np.zeros((blocks, BS, KVH, D), np.uint16)
+    vc = np.zeros_like(kc)
+    lib = ora.lib()
+    res = np.empty((T, H), np.uint16)
+    normed = np.empty((T, H), np.uint16)
+    query = np.empty((T, QH, D), np.uint16)
+    act = np.empty((T, I), np.uint16)
+    p = lambda a: a.ctypes.data  # noqa: E731
+
+    def step(nlayers):
+        lib.ora_embedding(p(tok), p(table), p(res), T, H, V, threads)
+        for i in range(nlayers):
+            if i == 0:
+                lib.ora_rms(p(res), p(wn), p(normed), T, H, EPS, threads)
+            else:
+                lib.ora_add_rms(p(x_mlp), p(res), p(wn), p(normed), T, H, EPS, threads)
+            lib.ora_qkv_rope(p(qkv), p(qn), p(kn), p(pos), p(slots), p(query), p(kc), p(vc), T, QH, KVH, D, BS, blocks,
+                             EPS, 1.0, p(rope), MAX_POS, threads)
+            lib.ora_add_rms(p(x_attn), p(res), p(wn), p(normed), T, H, EPS, threads)
+            lib.ora_silu(p(gu), p(act), T, I, threads)
+        lib.ora_add_rms(p(x_mlp), p(res), p(wn), p(normed), T, H, EPS, threads)
+
+    step(1)  # warm-up
+    runs = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        step(layers)
+        runs.append(time.perf_counter() - t0)
+    sec = float(np.median(runs))
+    return {"value": T / sec, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle C restatement, full step ({layers} layers, T={T}; per-layer inputs shared), "
+                      f"median of {len(runs)} runs = {sec * 1e3:.1f} ms/step"}
+
+
+# ------------------------------------------------------------------ main ---
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=8192)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
+    ap.add_argument("--kernel-rounds", type=int, default=5)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported "
+              "(the kernels are per-token; a data-parallel split needs no collectives).", file=sys.stderr)
+        return 2
+
+    hip = Hip()
+    gpu = nvr.Gpu(0)
+    fill = Filler(gpu, hip)
+    chain = Chain(gpu, fill, args.tokens, LAYERS)
+    gpu.sync()
+    graph = gpu.capture(chain.step)
+    ms = time_graph(gpu, hip, graph, args.steps, args.warmup)
+    tokens_per_s = args.tokens / (ms / 1e3)
+    chain_gbs = chain.bytes() / (ms / 1e3) / 1e9
+
+    kernels = {}
+    if not args.no_kernels:
+        for name, workload, launches, nbytes, rows in kernel_cases(gpu, fill, chain):
+            t = run_kernel_case(gpu, hip, launches, args.kernel_rounds)
+            gbs = nbytes / (t / 1e3) / 1e9
+            kernels[name] = {"workload": workload, "us": round(t * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
+                             "frac": round(gbs / HBM_PEAK_GBS, 4), "rows_per_s": round(rows / (t / 1e3), 1),
+                             "launches": len(launches)}
+
+    # Dominant kernel of the step: largest launches x time at the step's shape.
+    roofline = None
+    if kernels:
+        shape_of = {"add_rms": "add_rms_8192x1024", "qkv_rope_cached": "qkv_rope_8192", "silu": "silu_8192x6144"}
+        share = {k: chain.launches()[k] * kernels[v]["us"] for k, v in shape_of.items() if v in kernels}
+        dom = max(share, key=share.get)
+        kd = kernels[shape_of[dom]]
+        roofline = {"kernel": shape_of[dom], "bound": "hbm", "achieved": kd["GB/s"], "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": kd["frac"], "traffic": None}
+
+    cpu = None
+    if not args.no_cpu:
+        threads = max(1, min(16, os.cpu_count() or 1))
+        cpu = cpu_baseline(args.tokens, LAYERS, threads)
+
+    line = {
+        "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "Qwen3-0.6B fused per-layer kernel chain: embedding + 28 x [add-RMSNorm, q/k-norm + "
+                               "RoPE + paged KV write, add-RMSNorm, SiLU-mul] + final add-RMSNorm, one HIP graph",
+                   "tokens": args.tokens, "layers": LAYERS, "hidden": H, "intermediate": I, "q_heads": QH,
+                   "kv_heads": KVH, "head_dim": D, "block_size": BS, "parallelism": "none (1 GPU)"},
+        "step_GB/s": round(chain_gbs, 1), "step_hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4),
+        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

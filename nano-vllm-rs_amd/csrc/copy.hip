@@ -27,18 +27,18 @@ __device__ __forceinline__ void copy_row16(const uint4* __restrict__ src, uint4*
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int c = c0 + u * kWave;
-            if (c < chunks) v[u] = src[c];
+            if (c < chunks) v[u] = nvr::load_stream(src + c);
         }
 #pragma unroll
         for (int u = 0; u < kUnroll; ++u) {
             const int c = c0 + u * kWave;
-            if (c < chunks) dst[c] = v[u];
+            if (c < chunks) nvr::store_stream(dst + c, v[u]);
         }
     }
 }
 
 __device__ __forceinline__ void zero_row16(uint4* __restrict__ dst, int chunks, int lane) {
-    for (int c = lane; c < chunks; c += kWave) dst[c] = make_uint4(0, 0, 0, 0);
+    for (int c = lane; c < chunks; c += kWave) nvr::store_stream(dst + c, make_uint4(0, 0, 0, 0));
 }
 
 // out[r] = src[index[r]] (or zeros); rows of `hidden` bf16, `hidden % 8 == 0`.
@@ -85,12 +85,12 @@ __global__ __launch_bounds__(256) void kv_write16(const uint16_t* __restrict__ k
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int c = c0 + u * kWave;
-            if (c < chunks) { a[u] = ks[c]; b[u] = vs[c]; }
+            if (c < chunks) { a[u] = nvr::load_stream(ks + c); b[u] = nvr::load_stream(vs + c); }
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const int c = c0 + u * kWave;
-            if (c < chunks) { kd[c] = a[u]; vd[c] = b[u]; }
+            if (c < chunks) { nvr::store_stream(kd + c, a[u]); nvr::store_stream(vd + c, b[u]); }
         }
     }
 }

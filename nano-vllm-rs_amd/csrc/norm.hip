@@ -44,11 +44,11 @@ __global__ __launch_bounds__(256) void rms_rows_fast(const uint16_t* __restrict_
     if (active) {
         uint4 xw[K];
 #pragma unroll
-        for (int k = 0; k < K; ++k) xw[k] = *reinterpret_cast<const uint4*>(x + base + 256 * k);
+        for (int k = 0; k < K; ++k) xw[k] = nvr::load_stream(x + base + 256 * k);
         if constexpr (ADD) {
             uint4 rw[K];
 #pragma unroll
-            for (int k = 0; k < K; ++k) rw[k] = *reinterpret_cast<const uint4*>(residual + base + 256 * k);
+            for (int k = 0; k < K; ++k) rw[k] = nvr::load_stream(residual + base + 256 * k);
 #pragma unroll
             for (int k = 0; k < K; ++k) {
                 float a[8], b[8];
@@ -100,8 +100,8 @@ __global__ __launch_bounds__(256) void rms_rows_fast(const uint16_t* __restrict_
         nvr::unpack8(*reinterpret_cast<const uint4*>(weight + 256 * k + 8 * m), wf);
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = (v[k][i] * inv) * wf[i];
-        if constexpr (ADD) *reinterpret_cast<uint4*>(residual + base + 256 * k) = nvr::pack8(v[k]);
-        *reinterpret_cast<uint4*>(out + base + 256 * k) = nvr::pack8(o);
+        if constexpr (ADD) nvr::store_stream(residual + base + 256 * k, nvr::pack8(v[k]));
+        nvr::store_stream(out + base + 256 * k, nvr::pack8(o));
     }
 }
 

@@ -44,6 +44,19 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
                       pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
 }
 
+// Streaming 16-byte accesses (non-temporal hint on the global load/store) for
+// data each launch touches exactly once; on MI355X they keep the caches for
+// the reused operands and raise copy bandwidth by roughly 7-40% per kernel.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const void* p) {
+    const u32x4_t v = __builtin_nontemporal_load(static_cast<const u32x4_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store_stream(void* p, const uint4& v) {
+    const u32x4_t w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, static_cast<u32x4_t*>(p));
+}
+
 // Round a float to bf16 precision and widen it back (the value a bf16 store
 // followed by a load would produce).
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }

@@ -41,21 +41,32 @@ __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict_
     constexpr int D = 128, HALF = 64;
     const int heads = qh + 2 * kvh;
     const int m = threadIdx.x & (kHeadLanes - 1);
-    const int64_t g = int64_t(blockIdx.x) * (blockDim.x / kHeadLanes) + threadIdx.x / kHeadLanes;
-    const int64_t row = g / heads;
-    const int head = int(g - row * heads);
+    // The block's first (row, head) pair comes from one scalar division; the
+    // 16 groups of the block then step through heads, wrapping into later rows.
+    const int64_t g0 = int64_t(blockIdx.x) * (blockDim.x / kHeadLanes);
+    const int64_t row0 = g0 / heads;
+    int head = int(g0 - row0 * heads) + int(threadIdx.x / kHeadLanes);
+    int64_t row = row0;
+    if (heads >= kHeadLanes) {
+        const bool wrap = head >= heads;
+        row += wrap ? 1 : 0;
+        head -= wrap ? heads : 0;
+    } else {
+        row += head / heads;
+        head %= heads;
+    }
     const bool active = row < rows;  // uniform across the 16-lane row
     const int64_t packed = row * heads * D;
 
     uint4 xw = make_uint4(0, 0, 0, 0);
-    if (active) xw = *reinterpret_cast<const uint4*>(qkv + packed + int64_t(head) * D + 8 * m);
+    if (active) xw = nvr::load_stream(qkv + packed + int64_t(head) * D + 8 * m);
     const int slot = active ? slots[row] : -1;
     const bool valid_slot = slot >= 0 && int64_t(slot) < int64_t(bs) * blocks;
 
     if (head >= qh + kvh) {  // V head: plain copy into the cache
         if (active && valid_slot) {
             const int local = head - qh - kvh;
-            *reinterpret_cast<uint4*>(vc + (int64_t(slot) * kvh + local) * D + 8 * m) = xw;
+            nvr::store_stream(vc + (int64_t(slot) * kvh + local) * D + 8 * m, xw);
         }
         return;  // the whole 16-lane row leaves together; no later shuffles cross rows
     }
@@ -123,9 +134,9 @@ __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict_
     if (!active) return;
     const uint4 packed_out = nvr::pack8(o);
     if (is_q) {
-        *reinterpret_cast<uint4*>(qout + (row * qh + local) * D + 8 * m) = packed_out;
+        nvr::store_stream(qout + (row * qh + local) * D + 8 * m, packed_out);
     } else if (valid_slot) {
-        *reinterpret_cast<uint4*>(kc + (int64_t(slot) * kvh + local) * D + 8 * m) = packed_out;
+        nvr::store_stream(kc + (int64_t(slot) * kvh + local) * D + 8 * m, packed_out);
     }
 }
 

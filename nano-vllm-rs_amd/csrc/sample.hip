@@ -80,14 +80,25 @@ __device__ __forceinline__ Best scan_range(const uint16_t* __restrict__ row, int
     Best b{-__builtin_inff(), nvr::kNoIndex};
     const bool gumbel = temperature > 0.0f;
     if constexpr (VEC) {
-        const uint4* chunks = reinterpret_cast<const uint4*>(row);
-        // 64-bit cursors: vocab may sit close to INT_MAX.
-        if (gumbel) {
-            for (int64_t t = begin + 8 * int64_t(threadIdx.x); t < end; t += 8 * int64_t(blockDim.x))
-                scan_chunk<true>(b, chunks[t / 8], int(t), temperature, seed);
-        } else {
-            for (int64_t t = begin + 8 * int64_t(threadIdx.x); t < end; t += 8 * int64_t(blockDim.x))
-                scan_chunk<false>(b, chunks[t / 8], int(t), temperature, seed);
+        // kLoads chunks of 8 logits per lane are in flight before any is
+        // scored; the scan order does not matter under the total order.
+        constexpr int kLoads = 4;
+        const int64_t step = 8 * int64_t(blockDim.x);
+        for (int64_t t0 = begin + 8 * int64_t(threadIdx.x); t0 < end; t0 += kLoads * step) {
+            uint4 w[kLoads];
+#pragma unroll
+            for (int u = 0; u < kLoads; ++u) {
+                const int64_t t = t0 + u * step;  // 64-bit: vocab may sit close to INT_MAX
+                if (t < end) w[u] = nvr::load_stream(row + t);
+            }
+#pragma unroll
+            for (int u = 0; u < kLoads; ++u) {
+                const int64_t t = t0 + u * step;
+                if (t < end) {
+                    if (gumbel) scan_chunk<true>(b, w[u], int(t), temperature, seed);
+                    else scan_chunk<false>(b, w[u], int(t), temperature, seed);
+                }
+            }
         }
     } else {
         for (int64_t t = begin + int64_t(threadIdx.x); t < end; t += int64_t(blockDim.x)) {

@@ -34,14 +34,14 @@ __global__ __launch_bounds__(256) void silu16(const uint16_t* __restrict__ packe
     const int chunks = intermediate / 8;
     if (chunk >= chunks) return;
     const int64_t gate_base = int64_t(row) * 2 * intermediate + 8 * chunk;
-    const uint4 gw = *reinterpret_cast<const uint4*>(packed + gate_base);
-    const uint4 uw = *reinterpret_cast<const uint4*>(packed + gate_base + intermediate);
+    const uint4 gw = nvr::load_stream(packed + gate_base);
+    const uint4 uw = nvr::load_stream(packed + gate_base + intermediate);
     float g[8], u[8], o[8];
     nvr::unpack8(gw, g);
     nvr::unpack8(uw, u);
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = silu_mul(g[i], u[i]);
-    *reinterpret_cast<uint4*>(out + int64_t(row) * intermediate + 8 * chunk) = nvr::pack8(o);
+    nvr::store_stream(out + int64_t(row) * intermediate + 8 * chunk, nvr::pack8(o));
 }
 
 __global__ __launch_bounds__(256) void silu_generic(const uint16_t* __restrict__ packed, uint16_t* __restrict__ out,

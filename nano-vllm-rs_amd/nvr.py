@@ -14,9 +14,11 @@ shared object is missing, every entry point raises.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import math
 import os
+import sys
 from typing import Callable, Iterable, Sequence
 
 import numpy as np
@@ -64,6 +66,22 @@ SIGNATURES = {
 }
 
 _LIB = None
+_EXITING = False
+
+
+def _mark_exiting() -> None:
+    # Runs before interpreter finalization: from here on, finalizers stop
+    # calling into the library, because module teardown destroys objects in
+    # an arbitrary order and the process exit releases device memory anyway.
+    global _EXITING
+    _EXITING = True
+
+
+atexit.register(_mark_exiting)
+
+
+def _native_ok() -> bool:
+    return not _EXITING and not sys.is_finalizing()
 
 
 class BackendError(RuntimeError):
@@ -136,9 +154,9 @@ class _Context:
             raise ValueError("allocation, transfer and synchronization are forbidden during graph capture")
 
     def __del__(self):
-        if getattr(self, "handle", None):
+        if getattr(self, "handle", None) and _native_ok():
             self.lib.nv_destroy(self.handle)
-            self.handle = None
+        self.handle = None
 
 
 class _Allocation:
@@ -148,9 +166,9 @@ class _Allocation:
         self.bytes = nbytes
 
     def __del__(self):
-        if getattr(self, "ptr", None):
+        if getattr(self, "ptr", None) and _native_ok() and self.context.handle:
             self.context.lib.nv_free(self.context.handle, self.ptr)
-            self.ptr = None
+        self.ptr = None
 
 
 class Buffer:
@@ -220,9 +238,9 @@ class Graph:
         _check(self.context.lib.nv_graph_replay(self.context.handle, self.handle))
 
     def __del__(self):
-        if getattr(self, "handle", None):
+        if getattr(self, "handle", None) and _native_ok() and self.context.handle:
             self.context.lib.nv_graph_destroy(self.context.handle, self.handle)
-            self.handle = None
+        self.handle = None
 
 
 class Gpu:
