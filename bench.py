@@ -233,42 +233,48 @@ def time_graph(gpu, hip, graph, reps, warmup):
 
 
 # ------------------------------------------------------ per-kernel loops ---
-def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain):
-    """Yields (name, workload, launch closures over rotating sets, bytes per launch, rows per launch)."""
+def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain, only=()):
+    """(name, workload, launch closures over rotating sets, bytes per launch, rows per launch) per case."""
     cases = []
+
+    def want(*names):
+        return not only or any(n in only for n in names)
 
     def sets_for(per_set_bytes):
         return max(3, -(-MALL_DEFEAT_BYTES // per_set_bytes))
 
-    # RMSNorm 8 x 1024 (latency-bound decode shape).
-    n = 64
-    xs = [fill.normal(8 * H * 2) for _ in range(n)]
     w = fill.normal(H * 2, 1.0, 0.02)
-    outs = [gpu.alloc(8 * H * 2) for _ in range(n)]
-    cases.append(("rms_8x1024", "RMSNorm x[8,1024]",
-                  [lambda i=i: gpu.rms_norm(xs[i], w, outs[i], 8, H, EPS) for i in range(n)], bytes_rms(8, H), 8))
+    # RMSNorm 8 x 1024 (latency-bound decode shape).
+    if want("rms_8x1024"):
+        n = 64
+        xs = [fill.normal(8 * H * 2) for _ in range(n)]
+        outs = [gpu.alloc(8 * H * 2) for _ in range(n)]
+        cases.append(("rms_8x1024", "RMSNorm x[8,1024]",
+                      [lambda i=i: gpu.rms_norm(xs[i], w, outs[i], 8, H, EPS) for i in range(n)], bytes_rms(8, H), 8))
 
     # add-RMSNorm 8192 x 1024.
     T = 8192
-    per = 3 * T * H * 2
-    s = sets_for(per)
-    ax = [fill.normal(T * H * 2) for _ in range(s)]
-    ar = [fill.normal(T * H * 2) for _ in range(s)]
-    ao = [gpu.alloc(T * H * 2) for _ in range(s)]
-    cases.append(("add_rms_8192x1024", "residual add + RMSNorm [8192,1024]",
-                  [lambda i=i, T=T: gpu.add_rms_norm(ax[i], ar[i], w, ao[i], T, H, EPS) for i in range(s)],
-                  bytes_add_rms(T, H), T))
+    if want("add_rms_8192x1024"):
+        s = sets_for(3 * T * H * 2)
+        ax = [fill.normal(T * H * 2) for _ in range(s)]
+        ar = [fill.normal(T * H * 2) for _ in range(s)]
+        ao = [gpu.alloc(T * H * 2) for _ in range(s)]
+        cases.append(("add_rms_8192x1024", "residual add + RMSNorm [8192,1024]",
+                      [lambda i=i, T=T: gpu.add_rms_norm(ax[i], ar[i], w, ao[i], T, H, EPS) for i in range(s)],
+                      bytes_add_rms(T, H), T))
 
     # SiLU 8192 x 6144 -> 8192 x 3072.
-    per = 3 * T * I * 2
-    s = sets_for(per)
-    gus = [fill.normal(T * 2 * I * 2, 0.0, 2.0) for _ in range(s)]
-    acts = [gpu.alloc(T * I * 2) for _ in range(s)]
-    cases.append(("silu_8192x6144", "SiLU(gate)*up [8192,6144] -> [8192,3072]",
-                  [lambda i=i, T=T: gpu.silu_mul(gus[i], acts[i], T, I) for i in range(s)], bytes_silu(T, I), T))
+    if want("silu_8192x6144"):
+        s = sets_for(3 * T * I * 2)
+        gus = [fill.normal(T * 2 * I * 2, 0.0, 2.0) for _ in range(s)]
+        acts = [gpu.alloc(T * I * 2) for _ in range(s)]
+        cases.append(("silu_8192x6144", "SiLU(gate)*up [8192,6144] -> [8192,3072]",
+                      [lambda i=i, T=T: gpu.silu_mul(gus[i], acts[i], T, I) for i in range(s)], bytes_silu(T, I), T))
 
     # q/k norm + RoPE + KV write at 2048 and 8192 tokens, uniform random positions.
     for T in (2048, 8192):
+        if not want(f"qkv_rope_{T}"):
+            continue
         rng = np.random.default_rng(T)
         pos = rng.integers(0, MAX_POS, T).astype(np.int32)
         blocks = T // BS
@@ -291,29 +297,32 @@ def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain):
 
     # Embedding gather, 16384 tokens from a [151936, 1024] table (three tables).
     T = 16384
-    tables = [chain.table] + [fill.normal(V * H * 2, 0.0, 0.02) for _ in range(2)]
-    toks = [fill.ints(np.random.default_rng(100 + j).integers(0, V, T)) for j in range(6)]
-    eouts = [gpu.alloc(T * H * 2) for _ in range(6)]
-    cases.append(("embedding_16384", "embedding gather, 16384 tokens, table [151936,1024]",
-                  [lambda j=j, T=T: gpu.embedding(toks[j], tables[j % 3], eouts[j], T, H, V) for j in range(6)],
-                  bytes_embedding(T, H), T))
+    if want("embedding_16384"):
+        tables = [chain.table] + [fill.normal(V * H * 2, 0.0, 0.02) for _ in range(2)]
+        toks = [fill.ints(np.random.default_rng(100 + j).integers(0, V, T)) for j in range(6)]
+        eouts = [gpu.alloc(T * H * 2) for _ in range(6)]
+        cases.append(("embedding_16384", "embedding gather, 16384 tokens, table [151936,1024]",
+                      [lambda j=j, T=T: gpu.embedding(toks[j], tables[j % 3], eouts[j], T, H, V) for j in range(6)],
+                      bytes_embedding(T, H), T))
 
     # Paged KV write, k/v [16384, 8, 128] into per-layer caches.
-    blocks = T // BS
-    per = 4 * T * KVH * D * 2
-    s = sets_for(per)
-    ks = [fill.normal(T * KVH * D * 2) for _ in range(s)]
-    vs = [fill.normal(T * KVH * D * 2) for _ in range(s)]
-    kcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
-    vcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
-    rng = np.random.default_rng(7)
-    perm = rng.permutation(blocks)
-    sl = fill.ints((perm[np.arange(T) // BS] * BS + np.arange(T) % BS).astype(np.int32))
-    cases.append(("kv_write_16384", "paged KV write k,v [16384,8,128]",
-                  [lambda i=i, T=T, blocks=blocks, ks=ks, vs=vs, kcs=kcs, vcs=vcs: gpu.kv_write(ks[i], vs[i], sl, kcs[i], vcs[i], T, KVH, D, BS, blocks)
-                   for i in range(s)], bytes_kv_write(T), T))
+    if want("kv_write_16384"):
+        blocks = T // BS
+        s = sets_for(4 * T * KVH * D * 2)
+        ks = [fill.normal(T * KVH * D * 2) for _ in range(s)]
+        vs = [fill.normal(T * KVH * D * 2) for _ in range(s)]
+        kcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
+        vcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
+        perm = np.random.default_rng(7).permutation(blocks)
+        sl = fill.ints((perm[np.arange(T) // BS] * BS + np.arange(T) % BS).astype(np.int32))
+        cases.append(("kv_write_16384", "paged KV write k,v [16384,8,128]",
+                      [lambda i=i, T=T, blocks=blocks: gpu.kv_write(ks[i], vs[i], sl, kcs[i], vcs[i], T, KVH, D, BS,
+                                                                   blocks) for i in range(s)],
+                      bytes_kv_write(T), T))
 
     # Sampling 256 x 151936: rows 0-127 greedy, 128-255 Gumbel at T=0.6.
+    if not want("sampling_256x151936", "sampling_greedy", "sampling_gumbel"):
+        return cases
     B = 256
     per = B * V * 2
     s = sets_for(per)
@@ -328,6 +337,8 @@ def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain):
     for name, temps, label in (("sampling_256x151936", mixed, "128 greedy + 128 Gumbel (T=0.6) rows"),
                                ("sampling_greedy", greedy, "256 greedy rows"),
                                ("sampling_gumbel", gumbel, "256 Gumbel rows (T=0.6)")):
+        if not want(name):
+            continue
         cases.append((name, f"sampling logits [256,151936], {label}",
                       [lambda i=i, temps=temps, B=B: gpu.sample_parallel(logits[i], temps, seeds, out, ps, pi, B, V)
                        for i in range(s)], bytes_sampling(B, V), B))
@@ -403,6 +414,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
     ap.add_argument("--kernel-rounds", type=int, default=5)
+    ap.add_argument("--only", default="", help="comma-separated kernel cases to run (implies --no-cpu, skips the step)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported "
@@ -412,16 +424,19 @@ def main() -> int:
     hip = Hip()
     gpu = nvr.Gpu(0)
     fill = Filler(gpu, hip)
-    chain = Chain(gpu, fill, args.tokens, LAYERS)
+    only = [k for k in args.only.split(",") if k]
+    chain = Chain(gpu, fill, args.tokens, 1 if only else LAYERS)
     gpu.sync()
-    graph = gpu.capture(chain.step)
-    ms = time_graph(gpu, hip, graph, args.steps, args.warmup)
+    ms = float("nan")
+    if not only:
+        graph = gpu.capture(chain.step)
+        ms = time_graph(gpu, hip, graph, args.steps, args.warmup)
     tokens_per_s = args.tokens / (ms / 1e3)
     chain_gbs = chain.bytes() / (ms / 1e3) / 1e9
 
     kernels = {}
     if not args.no_kernels:
-        for name, workload, launches, nbytes, rows in kernel_cases(gpu, fill, chain):
+        for name, workload, launches, nbytes, rows in kernel_cases(gpu, fill, chain, only):
             t = run_kernel_case(gpu, hip, launches, args.kernel_rounds)
             gbs = nbytes / (t / 1e3) / 1e9
             kernels[name] = {"workload": workload, "us": round(t * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
@@ -439,7 +454,7 @@ def main() -> int:
                     "unit": "GB/s", "frac": kd["frac"], "traffic": None}
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and not only:
         threads = max(1, min(16, os.cpu_count() or 1))
         cpu = cpu_baseline(args.tokens, LAYERS, threads)
 

@@ -20,6 +20,8 @@
 // (one HBM pass; the reference reads x and residual twice). In that layout
 //   warp level 16 -> lane m^2, level 8 -> lane m^1, levels 4/2/1 -> in-lane,
 //   block level 4 -> lane m^16, level 2 -> m^8, level 1 -> m^4.
+// (The cross-lane steps use LDS-crossbar shuffles; DPP variants and a
+// two-source bf16 pack measured slower for this kernel on MI355X.)
 // Generic path (any hidden, any alignment): one row per wave, lane l owns
 // reference threads 4l..4l+3 with 2-byte accesses.
 #include "../../include/nano_hip.h"
@@ -82,11 +84,7 @@ __global__ __launch_bounds__(256) void rms_rows_fast(const uint16_t* __restrict_
     for (int i = 0; i < 8; ++i) s[i] = s[i] + nvr::xor_lane(s[i], 2);
 #pragma unroll
     for (int i = 0; i < 8; ++i) s[i] = s[i] + nvr::xor_lane(s[i], 1);
-    float w4[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) w4[i] = s[i] + s[i + 4];
-    const float w2a = w4[0] + w4[2], w2b = w4[1] + w4[3];
-    float total = w2a + w2b;  // warp sum of warp m/4, in every lane of that warp
+    float total = ((s[0] + s[4]) + (s[2] + s[6])) + ((s[1] + s[5]) + (s[3] + s[7]));
     // Block tree over the 8 warp sums (lanes 0,4,...,28 of the half).
     total = total + nvr::xor_lane(total, 16);
     total = total + nvr::xor_lane(total, 8);
@@ -100,8 +98,8 @@ __global__ __launch_bounds__(256) void rms_rows_fast(const uint16_t* __restrict_
         nvr::unpack8(*reinterpret_cast<const uint4*>(weight + 256 * k + 8 * m), wf);
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = (v[k][i] * inv) * wf[i];
-        if constexpr (ADD) nvr::store_stream(residual + base + 256 * k, nvr::pack8(v[k]));
-        nvr::store_stream(out + base + 256 * k, nvr::pack8(o));
+        if constexpr (ADD) nvr::store_stream(residual + base + 256 * k, nvr::pack8_split(v[k]));
+        nvr::store_stream(out + base + 256 * k, nvr::pack8_split(o));
     }
 }
 

@@ -28,8 +28,17 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_floa
 __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
     return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
 }
-// Two floats -> two bf16 in one dword (lo in bits 0..15), round to nearest even.
+// Two floats -> two bf16 in one dword (lo in bits 0..15), round to nearest
+// even. pack_bf16x2 is one two-source v_cvt_pk_bf16_f32; pack_bf16x2_split
+// converts each half on its own and merges them. Both give the same bits;
+// which one schedules better is kernel-specific (measured per kernel).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const f32x2_t f = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+__device__ __forceinline__ uint32_t pack_bf16x2_split(float lo, float hi) {
     return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
 }
 // Widen 8 packed bf16 (one 16-byte load) into floats.
@@ -42,6 +51,10 @@ __device__ __forceinline__ void unpack8(const uint4& w, float* f) {
 __device__ __forceinline__ uint4 pack8(const float* f) {
     return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]),
                       pack_bf16x2(f[4], f[5]), pack_bf16x2(f[6], f[7]));
+}
+__device__ __forceinline__ uint4 pack8_split(const float* f) {
+    return make_uint4(pack_bf16x2_split(f[0], f[1]), pack_bf16x2_split(f[2], f[3]),
+                      pack_bf16x2_split(f[4], f[5]), pack_bf16x2_split(f[6], f[7]));
 }
 
 // Streaming 16-byte accesses (non-temporal hint on the global load/store) for
@@ -67,6 +80,27 @@ __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to
 // lane 0, because each level adds the same two operands (a+b == b+a).
 __device__ __forceinline__ float xor_lane(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 __device__ __forceinline__ int xor_lane(int v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// DPP lane permutations (data-parallel primitives: the operand is read from
+// another lane of the same 16-lane row, no LDS traffic, and the compiler folds
+// the move into the consuming VALU op when it can).
+constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppRowRor8 = 0x128;       // row_ror:8 : lane ^ 8 inside a 16-lane row
+constexpr int kDppRowHalfMirror = 0x141; // row_half_mirror: lane i <-> 7-i inside each 8 lanes
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xF, 0xF, false));
+}
+
+// lane ^ 16 inside each 32-lane half (ds_swizzle bitmask mode: and 0x1f, xor 0x10).
+__device__ __forceinline__ float swizzle_xor16(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
 
 // ------------------------------------------------------------- 1 / sqrt ----
 // Correctly rounded sqrt followed by a correctly rounded division: fixed bits

@@ -16,11 +16,11 @@
 //   v head:    vc[slot, h', :] = qkv[r, qh + kvh + h', :]  (bit copy)
 //   K and V are written only when 0 <= slot < bs * blocks.
 //
-// Fast path (dim = 128, 16-byte aligned): one (row, head) per 16-lane DPP row.
+// Fast path (dim = 128, 16-byte aligned): a head occupies a 16-lane DPP row.
 // Lane m holds elements 8m..8m+7 (one 16-byte load), i.e. reference threads
 // 8m..8m+7. Warp levels 16/8 -> lane m^2 / m^1, levels 4/2/1 in-lane; the warp
-// sums sit in lanes 0,4,8,12 and fold as (W0 + W2) + (W1 + W3) -> m^8, m^4.
-// The NeoX partner of element j lives in lane m^8 of the same 16-lane row.
+// sums sit in lanes 0,4,8,12 and fold as (W0 + W2) + (W1 + W3). The NeoX
+// partner of element j lives in lane m^8 of the same 16-lane row.
 #include "../../include/nano_hip.h"
 #include "nvr_device.h"
 #include "nvr_internal.h"
@@ -31,6 +31,51 @@ using nvr::kWave;
 
 constexpr int kHeadLanes = 16;
 
+// q/k head: RMSNorm in the reference's order, bf16 rounding, NeoX rotation.
+// Returns the rotated chunk of this lane (elements 8m..8m+7), packed. The
+// 16 lanes of a head form one DPP row: warp level 16 is quad lane ^2, level 8
+// quad lane ^1; the warp sums (lanes 0,4,8,12) fold as (W0 + W2) + (W1 + W3)
+// through row_ror:8 then row_half_mirror (each quad holds one replicated sum).
+// sn_signed is -sin for elements j < 64 and +sin above, so that
+// rot = n*c + p*sn_signed rounds exactly like (n*c) -/+ (p*sin).
+__device__ __forceinline__ uint4 norm_rotate_d128(const uint4& xw, const float* wf, const float* cs,
+                                                  const float* sn_signed, float eps) {
+    constexpr int D = 128;
+    float x[8];
+    nvr::unpack8(xw, x);
+    float s[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = x[i] * x[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = s[i] + nvr::dpp<nvr::kDppQuadXor2>(s[i]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = s[i] + nvr::dpp<nvr::kDppQuadXor1>(s[i]);
+    float total = ((s[0] + s[4]) + (s[2] + s[6])) + ((s[1] + s[5]) + (s[3] + s[7]));
+    total = total + nvr::dpp<nvr::kDppRowRor8>(total);
+    total = total + nvr::dpp<nvr::kDppRowHalfMirror>(total);
+    const float inv = nvr::inv_sqrt_rn(total / float(D) + eps);
+    float n[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) n[i] = (x[i] * inv) * wf[i];
+    const uint4 np = nvr::pack8(n);  // the bf16-materialised normalised head
+    nvr::unpack8(np, n);
+    uint4 pp;  // NeoX partner chunk (elements j +/- 64) from lane m ^ 8
+    pp.x = nvr::dpp<nvr::kDppRowRor8>(np.x);
+    pp.y = nvr::dpp<nvr::kDppRowRor8>(np.y);
+    pp.z = nvr::dpp<nvr::kDppRowRor8>(np.z);
+    pp.w = nvr::dpp<nvr::kDppRowRor8>(np.w);
+    float p[8];
+    nvr::unpack8(pp, p);
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = n[i] * cs[i] + p[i] * sn_signed[i];
+    return nvr::pack8(o);
+}
+
+// One token row per wave. Group g (16 lanes) of the wave owns heads g, g+4,
+// g+8, ...; lane m of a group holds elements 8m..8m+7 of each of its heads.
+// All of a lane's head loads are issued before any head is processed, and the
+// row's position, slot, cos/sin and norm weights are read once per row.
 template <bool CACHED>
 __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qw,
                                                      const uint16_t* __restrict__ kw, const int* __restrict__ positions,
@@ -38,72 +83,25 @@ __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict_
                                                      uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int rows,
                                                      int qh, int kvh, int bs, int blocks, float eps, float theta,
                                                      const float* __restrict__ table, int max_positions) {
-    constexpr int D = 128, HALF = 64;
+    constexpr int D = 128, HALF = 64, GROUPS = kWave / kHeadLanes, DEPTH = 8;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int grp = lane / kHeadLanes, m = lane & (kHeadLanes - 1);
+    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= rows) return;  // uniform per wave
     const int heads = qh + 2 * kvh;
-    const int m = threadIdx.x & (kHeadLanes - 1);
-    // The block's first (row, head) pair comes from one scalar division; the
-    // 16 groups of the block then step through heads, wrapping into later rows.
-    const int64_t g0 = int64_t(blockIdx.x) * (blockDim.x / kHeadLanes);
-    const int64_t row0 = g0 / heads;
-    int head = int(g0 - row0 * heads) + int(threadIdx.x / kHeadLanes);
-    int64_t row = row0;
-    if (heads >= kHeadLanes) {
-        const bool wrap = head >= heads;
-        row += wrap ? 1 : 0;
-        head -= wrap ? heads : 0;
-    } else {
-        row += head / heads;
-        head %= heads;
+    const uint16_t* src = qkv + row * heads * D + 8 * m;
+    // The first DEPTH heads of this group are loaded before anything that
+    // waits on memory (position -> table), so they overlap that latency.
+    uint4 xw[DEPTH];
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j) {
+        const int h = grp + GROUPS * j;
+        if (h < heads) xw[j] = nvr::load_stream(src + int64_t(h) * D);
     }
-    const bool active = row < rows;  // uniform across the 16-lane row
-    const int64_t packed = row * heads * D;
-
-    uint4 xw = make_uint4(0, 0, 0, 0);
-    if (active) xw = nvr::load_stream(qkv + packed + int64_t(head) * D + 8 * m);
-    const int slot = active ? slots[row] : -1;
+    const int pos = positions[row];
+    const int slot = slots[row];
     const bool valid_slot = slot >= 0 && int64_t(slot) < int64_t(bs) * blocks;
 
-    if (head >= qh + kvh) {  // V head: plain copy into the cache
-        if (active && valid_slot) {
-            const int local = head - qh - kvh;
-            nvr::store_stream(vc + (int64_t(slot) * kvh + local) * D + 8 * m, xw);
-        }
-        return;  // the whole 16-lane row leaves together; no later shuffles cross rows
-    }
-
-    const bool is_q = head < qh;
-    const int local = is_q ? head : head - qh;
-    float x[8];
-    nvr::unpack8(xw, x);
-    // Thread-level partials are single squares; warp tree across lanes m^2, m^1.
-    float s[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s[i] = x[i] * x[i];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s[i] = s[i] + __shfl_xor(s[i], 2, kHeadLanes);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s[i] = s[i] + __shfl_xor(s[i], 1, kHeadLanes);
-    float total = ((s[0] + s[4]) + (s[2] + s[6])) + ((s[1] + s[5]) + (s[3] + s[7]));
-    total = total + __shfl_xor(total, 8, kHeadLanes);
-    total = total + __shfl_xor(total, 4, kHeadLanes);
-    const float inv = nvr::inv_sqrt_rn(total / float(D) + eps);
-
-    const uint16_t* w = is_q ? qw : kw;
-    float wf[8], n[8];
-    nvr::unpack8(*reinterpret_cast<const uint4*>(w + 8 * m), wf);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) n[i] = nvr::round_bf16((x[i] * inv) * wf[i]);
-    // Partner half of the NeoX pair, exchanged as packed bf16.
-    const uint4 mine = nvr::pack8(n);
-    uint4 other;
-    other.x = __shfl_xor(mine.x, 8, kHeadLanes);
-    other.y = __shfl_xor(mine.y, 8, kHeadLanes);
-    other.z = __shfl_xor(mine.z, 8, kHeadLanes);
-    other.w = __shfl_xor(mine.w, 8, kHeadLanes);
-    float p[8];
-    nvr::unpack8(other, p);
-
-    const int pos = active ? positions[row] : 0;
     const int pair0 = 8 * (m & 7);
     float cs[8], sn[8];
     if constexpr (CACHED) {
@@ -123,20 +121,35 @@ __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict_
 #pragma unroll
         for (int i = 0; i < 8; ++i) nvr::rope_cos_sin(pos, pair0 + i, D, theta, &cs[i], &sn[i]);
     }
-    const bool low = m < 8;  // elements j < dim/2
-    float o[8];
+    if (m < 8) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float a = n[i] * cs[i];
-        const float b = p[i] * sn[i];
-        o[i] = low ? a - b : a + b;
+        for (int i = 0; i < 8; ++i) sn[i] = -sn[i];
     }
-    if (!active) return;
-    const uint4 packed_out = nvr::pack8(o);
-    if (is_q) {
-        nvr::store_stream(qout + (row * qh + local) * D + 8 * m, packed_out);
-    } else if (valid_slot) {
-        nvr::store_stream(kc + (int64_t(slot) * kvh + local) * D + 8 * m, packed_out);
+    float qwf[8], kwf[8];
+    nvr::unpack8(*reinterpret_cast<const uint4*>(qw + 8 * m), qwf);
+    nvr::unpack8(*reinterpret_cast<const uint4*>(kw + 8 * m), kwf);
+
+    for (int h0 = grp; h0 < heads; h0 += GROUPS * DEPTH) {
+        if (h0 != grp) {
+#pragma unroll
+            for (int j = 0; j < DEPTH; ++j) {
+                const int h = h0 + GROUPS * j;
+                if (h < heads) xw[j] = nvr::load_stream(src + int64_t(h) * D);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < DEPTH; ++j) {
+            const int h = h0 + GROUPS * j;
+            if (h >= heads) break;
+            if (h >= qh + kvh) {  // V head: bit copy into the cache
+                if (valid_slot) nvr::store_stream(vc + (int64_t(slot) * kvh + (h - qh - kvh)) * D + 8 * m, xw[j]);
+            } else if (h < qh) {
+                nvr::store_stream(qout + (row * qh + h) * D + 8 * m, norm_rotate_d128(xw[j], qwf, cs, sn, eps));
+            } else {
+                const uint4 rot = norm_rotate_d128(xw[j], kwf, cs, sn, eps);
+                if (valid_slot) nvr::store_stream(kc + (int64_t(slot) * kvh + (h - qh)) * D + 8 * m, rot);
+            }
+        }
     }
 }
 
@@ -256,8 +269,7 @@ int launch_qkv_rope(nv_context* c, const void* qkv, const void* qw, const void* 
                      nvr::aligned(qout, 16) && nvr::aligned(kc, 16) && nvr::aligned(vc, 16) &&
                      (!CACHED || nvr::aligned(table, 16));
     if (vec) {
-        const int64_t nblocks = (pairs + 15) / 16;
-        if (nblocks > 0x7fffffff) return nvr::fail(-2, "qkv_rope: too many rows for one launch");
+        const int64_t nblocks = (int64_t(rows) + 3) / 4;
         hipLaunchKernelGGL((qkv_rope_d128<CACHED>), dim3(unsigned(nblocks)), dim3(256), 0, c->stream, q16, qw16,
                            kw16, pos, sl, qo, k16, v16, rows, qh, kvh, bs, blocks, eps, theta, tab, max_positions);
     } else {

@@ -26,6 +26,25 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return act * u;
 }
 
+// Eight elements on the reciprocal path, with one branch for the whole chunk
+// into the exact division (only taken when some gate is below about -87).
+__device__ __forceinline__ void silu_mul8(const float* g, const float* u, float* o) {
+    float d[8];
+    bool slow = false;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        d[i] = 1.0f + __builtin_amdgcn_exp2f(-g[i] * 1.44269504088896340736f);
+        slow |= !(d[i] < 0x1.0p126f);
+    }
+    if (__builtin_expect(slow, 0)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = silu_mul(g[i], u[i]);
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (g[i] * __builtin_amdgcn_rcpf(d[i])) * u[i];
+}
+
 __global__ __launch_bounds__(256) void silu16(const uint16_t* __restrict__ packed, uint16_t* __restrict__ out,
                                               int intermediate, int blocks_per_row) {
     const int row = blockIdx.x / blocks_per_row;
@@ -39,9 +58,8 @@ __global__ __launch_bounds__(256) void silu16(const uint16_t* __restrict__ packe
     float g[8], u[8], o[8];
     nvr::unpack8(gw, g);
     nvr::unpack8(uw, u);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = silu_mul(g[i], u[i]);
-    nvr::store_stream(out + int64_t(row) * intermediate + 8 * chunk, nvr::pack8(o));
+    silu_mul8(g, u, o);
+    nvr::store_stream(out + int64_t(row) * intermediate + 8 * chunk, nvr::pack8_split(o));
 }
 
 __global__ __launch_bounds__(256) void silu_generic(const uint16_t* __restrict__ packed, uint16_t* __restrict__ out,

@@ -111,9 +111,9 @@ def library(path: str | None = None) -> ctypes.CDLL:
     return lib
 
 
-def _check(code: int) -> None:
+def _check(code: int, lib: ctypes.CDLL | None = None) -> None:
     if code != 0:
-        msg = library().nv_last_error().decode(errors="replace")
+        msg = (lib or library()).nv_last_error().decode(errors="replace")
         raise BackendError(msg, code)
 
 
@@ -143,11 +143,11 @@ def sampling_seed(base: int, request_id: int, generated: int) -> int:
 
 
 class _Context:
-    def __init__(self, handle: int):
+    def __init__(self, handle: int, lib: ctypes.CDLL):
         self.handle = handle
         self.capturing = False
         self.captured: list[Buffer] = []
-        self.lib = library()
+        self.lib = lib
 
     def outside_capture(self) -> None:
         if self.capturing:
@@ -246,15 +246,18 @@ class Graph:
 class Gpu:
     """One device, one stream, one hipBLAS handle (src/gpu.rs:394-1112)."""
 
-    def __init__(self, device: int = 0):
+    def __init__(self, device: int = 0, library_path: str | None = None):
+        """library_path selects another build of libnano_hip.so (default: this directory's)."""
         if device < 0:
             raise ValueError("device index must be nonnegative")
-        lib = library()
+        lib = library(library_path)
         handle = _vp()
-        _check(lib.nv_create(device, ctypes.byref(handle)))
+        code = lib.nv_create(device, ctypes.byref(handle))
+        if code != 0:
+            raise BackendError(lib.nv_last_error().decode(errors="replace"), code)
         if not handle.value:
             raise BackendError("library returned a null context", -1)
-        self.context = _Context(handle.value)
+        self.context = _Context(handle.value, lib)
         self.lib = lib
 
     @property
