@@ -13,11 +13,11 @@
 // and GPU agree on every Gumbel index.
 //
 // Layout: stage 1 gives each (row, partition) one 256-thread block; every lane
-// reads 16-byte chunks (8 logits) and keeps its own best (score, index); the
-// wave folds with butterfly shuffles and the four waves through LDS. Stage 2
-// folds a row's partials in one wave. The partition width is a multiple of the
-// reference's 2048, chosen so the batch still fills the GPU; the caller's
-// scratch (batch x ceil(vocab/2048) entries) always suffices.
+// loads kChunksPerLane 16-byte chunks (8 logits each) up front, keeps its own
+// best (score, index), the wave folds with butterfly shuffles and the four
+// waves through LDS. Stage 2 folds a row's partials in one wave. Partitions
+// are a multiple of the reference's 2048 tokens, so the caller's scratch
+// (batch x ceil(vocab/2048) entries) always suffices.
 #include "../../include/nano_hip.h"
 #include "nvr_device.h"
 #include "nvr_internal.h"
@@ -26,6 +26,10 @@ namespace {
 
 using nvr::kWave;
 constexpr int kRefPartition = 2048;
+// 16-byte chunks of logits per lane in a partition (partition width
+// 2048 * kChunksPerLane tokens). Measured on MI355X at 256 x 151936: 2 is the
+// best for Gumbel and mixed batches (4 favours all-greedy batches by ~7%).
+constexpr int kChunksPerLane = 2;
 
 struct Best {
     float score;
@@ -72,16 +76,14 @@ __device__ __forceinline__ void scan_chunk(Best& b, const uint4& w, int token0, 
     }
 }
 
-// Scans tokens [begin, end) of one row with 256 threads; begin and end are
-// multiples of 8 when VEC.
+// Scans tokens [begin, end) of one row with 256 threads (serial and generic
+// paths); begin and end are multiples of 8 when VEC.
 template <bool VEC>
 __device__ __forceinline__ Best scan_range(const uint16_t* __restrict__ row, int begin, int end, float temperature,
                                            uint64_t seed) {
     Best b{-__builtin_inff(), nvr::kNoIndex};
     const bool gumbel = temperature > 0.0f;
     if constexpr (VEC) {
-        // kLoads chunks of 8 logits per lane are in flight before any is
-        // scored; the scan order does not matter under the total order.
         constexpr int kLoads = 4;
         const int64_t step = 8 * int64_t(blockDim.x);
         for (int64_t t0 = begin + 8 * int64_t(threadIdx.x); t0 < end; t0 += kLoads * step) {
@@ -120,18 +122,62 @@ __global__ __launch_bounds__(256) void sample_rows(const uint16_t* __restrict__ 
     if (threadIdx.x == 0) out[r] = b.index == nvr::kNoIndex ? 0 : b.index;
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(256) void sample_partitions(const uint16_t* __restrict__ logits,
-                                                         const float* __restrict__ temps,
-                                                         const uint64_t* __restrict__ seeds,
-                                                         float* __restrict__ partial_scores,
-                                                         int* __restrict__ partial_ids, int vocab, int width,
-                                                         int parts) {
+// One partition of one row per 256-thread block. Each lane keeps C chunks of
+// 8 logits in registers (partition width 2048*C tokens) with every load issued
+// before any is scored; greedy rows compare, Gumbel rows score all 8*C tokens
+// with the 8 independent hash/log chains of a chunk interleaved.
+template <int C>
+__global__ __launch_bounds__(256) void sample_partitions_vec(const uint16_t* __restrict__ logits,
+                                                             const float* __restrict__ temps,
+                                                             const uint64_t* __restrict__ seeds,
+                                                             float* __restrict__ partial_scores,
+                                                             int* __restrict__ partial_ids, int vocab, int parts) {
+    constexpr int W = 2048 * C;
+    const int r = blockIdx.x / parts;
+    const int p = blockIdx.x - r * parts;
+    const int begin = p * W;
+    const int end = int(min(int64_t(begin) + W, int64_t(vocab)));
+    const uint16_t* row = logits + int64_t(r) * vocab;
+
+    uint4 w[C];
+    int t0[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        t0[c] = begin + 8 * int(threadIdx.x) + 2048 * c;
+        if (t0[c] < end) w[c] = nvr::load_stream(row + t0[c]);
+    }
+    const float temperature = temps[r];
+    const uint64_t seed = seeds[r];
+    Best b{-__builtin_inff(), nvr::kNoIndex};
+    if (temperature > 0.0f) {
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            if (t0[c] < end) scan_chunk<true>(b, w[c], t0[c], temperature, seed);
+    } else {
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            if (t0[c] < end) scan_chunk<false>(b, w[c], t0[c], temperature, seed);
+    }
+    b = block_argmax(b);
+    if (threadIdx.x == 0) {
+        partial_scores[blockIdx.x] = b.score;
+        partial_ids[blockIdx.x] = b.index;
+    }
+}
+
+// Generic partitions (unaligned rows or vocab % 8 != 0): 2048-token
+// partitions scanned element by element.
+__global__ __launch_bounds__(256) void sample_partitions_generic(const uint16_t* __restrict__ logits,
+                                                                 const float* __restrict__ temps,
+                                                                 const uint64_t* __restrict__ seeds,
+                                                                 float* __restrict__ partial_scores,
+                                                                 int* __restrict__ partial_ids, int vocab, int width,
+                                                                 int parts) {
     const int r = blockIdx.x / parts;
     const int p = blockIdx.x - r * parts;
     const int begin = p * width;
     const int end = int(min(int64_t(begin) + width, int64_t(vocab)));
-    Best b = scan_range<VEC>(logits + int64_t(r) * vocab, begin, end, temps[r], seeds[r]);
+    Best b = scan_range<false>(logits + int64_t(r) * vocab, begin, end, temps[r], seeds[r]);
     b = block_argmax(b);
     if (threadIdx.x == 0) {
         partial_scores[blockIdx.x] = b.score;
@@ -149,7 +195,11 @@ __global__ __launch_bounds__(64) void sample_combine(const float* __restrict__ p
     if (threadIdx.x == 0) out[blockIdx.x] = b.index == nvr::kNoIndex ? 0 : b.index;
 }
 
-bool vector_rows(const void* logits, int vocab) { return vocab % 8 == 0 && nvr::aligned(logits, 16); }
+// 16-byte row accesses need rows that start 16-byte aligned; token offsets
+// inside a partition stay below INT_MAX when vocab leaves 8192 of headroom.
+bool vector_rows(const void* logits, int vocab) {
+    return vocab % 8 == 0 && vocab <= 0x7fffffff - 8192 && nvr::aligned(logits, 16);
+}
 
 int launch_serial(nv_context* c, const void* logits, const void* temps, const void* seeds, void* out, int batch,
                   int vocab) {
@@ -182,28 +232,22 @@ int nv_sample_parallel(nv_context* c, const void* logits, const void* temps, con
     const int64_t ref_parts = (int64_t(vocab) + kRefPartition - 1) / kRefPartition;
     if (ref_parts <= 1 || int64_t(batch) * ref_parts > 0x7fffffff)
         return launch_serial(c, logits, temps, seeds, out, batch, vocab);
-    // Widen partitions (x2 steps, up to 16384 tokens) while the batch keeps at
-    // least four blocks per compute unit; never more partitions than scratch.
-    int width = kRefPartition;
-    const int64_t want_blocks = 4 * int64_t(c->cu_count > 0 ? c->cu_count : 256);
-    while (width < 16384) {
-        const int64_t parts = (int64_t(vocab) + 2 * width - 1) / (2 * width);
-        if (int64_t(batch) * parts < want_blocks) break;
-        width *= 2;
-    }
-    const int parts = int((int64_t(vocab) + width - 1) / width);
     auto l16 = static_cast<const uint16_t*>(logits);
     auto t = static_cast<const float*>(temps);
     auto s = static_cast<const uint64_t*>(seeds);
     auto ps = static_cast<float*>(partial_scores);
     auto pi = static_cast<int*>(partial_ids);
-    const dim3 grid(unsigned(int64_t(batch) * parts));
-    if (vector_rows(logits, vocab))
-        hipLaunchKernelGGL(sample_partitions<true>, grid, dim3(256), 0, c->stream, l16, t, s, ps, pi, vocab, width,
-                           parts);
-    else
-        hipLaunchKernelGGL(sample_partitions<false>, grid, dim3(256), 0, c->stream, l16, t, s, ps, pi, vocab, width,
-                           parts);
+    int parts;
+    if (vector_rows(logits, vocab)) {
+        // Never more partitions than the scratch holds (ceil(vocab / 2048)).
+        parts = int((int64_t(vocab) + 2048 * kChunksPerLane - 1) / (2048 * kChunksPerLane));
+        hipLaunchKernelGGL(sample_partitions_vec<kChunksPerLane>, dim3(unsigned(int64_t(batch) * parts)), dim3(256), 0,
+                           c->stream, l16, t, s, ps, pi, vocab, parts);
+    } else {
+        parts = int(ref_parts);
+        hipLaunchKernelGGL(sample_partitions_generic, dim3(unsigned(int64_t(batch) * parts)), dim3(256), 0, c->stream,
+                           l16, t, s, ps, pi, vocab, kRefPartition, parts);
+    }
     NVR_HIP(hipGetLastError());
     hipLaunchKernelGGL(sample_combine, dim3(batch), dim3(64), 0, c->stream, ps, pi, static_cast<int*>(out), parts);
     return nvr::launch_status();
