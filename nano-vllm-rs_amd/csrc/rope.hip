@@ -72,10 +72,12 @@ __device__ __forceinline__ uint4 norm_rotate_d128(const uint4& xw, const float* 
     return nvr::pack8(o);
 }
 
-// One token row per wave. Group g (16 lanes) of the wave owns heads g, g+4,
-// g+8, ...; lane m of a group holds elements 8m..8m+7 of each of its heads.
-// All of a lane's head loads are issued before any head is processed, and the
-// row's position, slot, cos/sin and norm weights are read once per row.
+// Two waves per token row. The row's heads form quads 4Q..4Q+3; wave half
+// hw takes quads hw, hw+2, hw+4, ... (for 16 q + 8 k + 8 v heads each half
+// gets 8 q, 4 k and 4 v heads), and group g (16 lanes) of the wave takes head
+// 4Q + g of each of its quads. Lane m of a group holds elements 8m..8m+7 of a
+// head. All head loads of a lane are issued first; position, slot, cos/sin
+// and the norm weights are read once per wave.
 template <bool CACHED>
 __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qw,
                                                      const uint16_t* __restrict__ kw, const int* __restrict__ positions,
@@ -83,19 +85,21 @@ __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict_
                                                      uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int rows,
                                                      int qh, int kvh, int bs, int blocks, float eps, float theta,
                                                      const float* __restrict__ table, int max_positions) {
-    constexpr int D = 128, HALF = 64, GROUPS = kWave / kHeadLanes, DEPTH = 8;
+    constexpr int D = 128, HALF = 64, GROUPS = kWave / kHeadLanes, DEPTH = 4, SPLIT = 2;
     const int lane = threadIdx.x & (kWave - 1);
     const int grp = lane / kHeadLanes, m = lane & (kHeadLanes - 1);
-    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const int64_t wave = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const int64_t row = wave / SPLIT;
+    const int hw = int(wave - row * SPLIT);
     if (row >= rows) return;  // uniform per wave
     const int heads = qh + 2 * kvh;
     const uint16_t* src = qkv + row * heads * D + 8 * m;
-    // The first DEPTH heads of this group are loaded before anything that
-    // waits on memory (position -> table), so they overlap that latency.
+    // Head of slot j in pass `pass`: quad hw + SPLIT * (j + DEPTH * pass).
+    auto head_of = [&](int pass, int j) { return GROUPS * (hw + SPLIT * (j + DEPTH * pass)) + grp; };
     uint4 xw[DEPTH];
 #pragma unroll
     for (int j = 0; j < DEPTH; ++j) {
-        const int h = grp + GROUPS * j;
+        const int h = head_of(0, j);
         if (h < heads) xw[j] = nvr::load_stream(src + int64_t(h) * D);
     }
     const int pos = positions[row];
@@ -129,18 +133,19 @@ __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict_
     nvr::unpack8(*reinterpret_cast<const uint4*>(qw + 8 * m), qwf);
     nvr::unpack8(*reinterpret_cast<const uint4*>(kw + 8 * m), kwf);
 
-    for (int h0 = grp; h0 < heads; h0 += GROUPS * DEPTH) {
-        if (h0 != grp) {
+    // Uniform trip count: a pass runs while its first quad exists.
+    for (int pass = 0; GROUPS * (hw + SPLIT * DEPTH * pass) < heads; ++pass) {
+        if (pass > 0) {  // rows with more than 32 heads
 #pragma unroll
             for (int j = 0; j < DEPTH; ++j) {
-                const int h = h0 + GROUPS * j;
+                const int h = head_of(pass, j);
                 if (h < heads) xw[j] = nvr::load_stream(src + int64_t(h) * D);
             }
         }
 #pragma unroll
         for (int j = 0; j < DEPTH; ++j) {
-            const int h = h0 + GROUPS * j;
-            if (h >= heads) break;
+            const int h = head_of(pass, j);
+            if (h >= heads) continue;
             if (h >= qh + kvh) {  // V head: bit copy into the cache
                 if (valid_slot) nvr::store_stream(vc + (int64_t(slot) * kvh + (h - qh - kvh)) * D + 8 * m, xw[j]);
             } else if (h < qh) {
@@ -269,7 +274,7 @@ int launch_qkv_rope(nv_context* c, const void* qkv, const void* qw, const void* 
                      nvr::aligned(qout, 16) && nvr::aligned(kc, 16) && nvr::aligned(vc, 16) &&
                      (!CACHED || nvr::aligned(table, 16));
     if (vec) {
-        const int64_t nblocks = (int64_t(rows) + 3) / 4;
+        const int64_t nblocks = (int64_t(rows) * 2 + 3) / 4;  // two waves per row
         hipLaunchKernelGGL((qkv_rope_d128<CACHED>), dim3(unsigned(nblocks)), dim3(256), 0, c->stream, q16, qw16,
                            kw16, pos, sl, qo, k16, v16, rows, qh, kvh, bs, blocks, eps, theta, tab, max_positions);
     } else {
