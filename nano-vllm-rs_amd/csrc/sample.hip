@@ -12,12 +12,17 @@
 // ln is nvr_logf, a fixed-bits logarithm shared with the host oracle, so CPU
 // and GPU agree on every Gumbel index.
 //
-// Layout: stage 1 gives each (row, partition) one 256-thread block; every lane
-// loads kChunksPerLane 16-byte chunks (8 logits each) up front, keeps its own
-// best (score, index), the wave folds with butterfly shuffles and the four
-// waves through LDS. Stage 2 folds a row's partials in one wave. Partitions
-// are a multiple of the reference's 2048 tokens, so the caller's scratch
-// (batch x ceil(vocab/2048) entries) always suffices.
+// Layout of nv_sample_parallel (16-byte aligned rows, vocab % 8 == 0):
+//   1. sample_partitions_vec: one 256-thread block per (row, partition of
+//      2048 * kChunksPerLane tokens); every lane loads its chunks of 8 logits
+//      up front; the block stores the partition's greedy maximum (greedy rows)
+//      or the exact Gumbel score of that token (Gumbel rows).
+//   2. sample_refine: Gumbel rows only. Exact pruning against the row's best
+//      partial, then the surviving tokens are scored (see the kernel).
+//   3. sample_combine: one wave folds a row's partials.
+// Partitions are a multiple of the reference's 2048 tokens, so the caller's
+// scratch (batch x ceil(vocab/2048) entries) always suffices. Other rows take
+// 2048-token partitions scanned element by element, then stage 3.
 #include "../../include/nano_hip.h"
 #include "nvr_device.h"
 #include "nvr_internal.h"
@@ -122,10 +127,12 @@ __global__ __launch_bounds__(256) void sample_rows(const uint16_t* __restrict__ 
     if (threadIdx.x == 0) out[r] = b.index == nvr::kNoIndex ? 0 : b.index;
 }
 
-// One partition of one row per 256-thread block. Each lane keeps C chunks of
-// 8 logits in registers (partition width 2048*C tokens) with every load issued
-// before any is scored; greedy rows compare, Gumbel rows score all 8*C tokens
-// with the 8 independent hash/log chains of a chunk interleaved.
+// First pass, every row: one partition of one row per 256-thread block. Each
+// lane keeps C chunks of 8 logits in registers (partition width 2048*C tokens)
+// with every load issued before any is compared. The block stores the
+// partition's greedy maximum, which is final for greedy rows; for Gumbel rows
+// it stores the exact Gumbel score of that maximum's token instead, which seeds
+// the pruning bound of sample_refine.
 template <int C>
 __global__ __launch_bounds__(256) void sample_partitions_vec(const uint16_t* __restrict__ logits,
                                                              const float* __restrict__ temps,
@@ -146,22 +153,127 @@ __global__ __launch_bounds__(256) void sample_partitions_vec(const uint16_t* __r
         t0[c] = begin + 8 * int(threadIdx.x) + 2048 * c;
         if (t0[c] < end) w[c] = nvr::load_stream(row + t0[c]);
     }
-    const float temperature = temps[r];
-    const uint64_t seed = seeds[r];
     Best b{-__builtin_inff(), nvr::kNoIndex};
-    if (temperature > 0.0f) {
 #pragma unroll
-        for (int c = 0; c < C; ++c)
-            if (t0[c] < end) scan_chunk<true>(b, w[c], t0[c], temperature, seed);
-    } else {
-#pragma unroll
-        for (int c = 0; c < C; ++c)
-            if (t0[c] < end) scan_chunk<false>(b, w[c], t0[c], temperature, seed);
-    }
+    for (int c = 0; c < C; ++c)
+        if (t0[c] < end) scan_chunk<false>(b, w[c], t0[c], 0.0f, 0);
     b = block_argmax(b);
     if (threadIdx.x == 0) {
-        partial_scores[blockIdx.x] = b.score;
+        const float temperature = temps[r];
+        float score = b.score;
+        if (temperature > 0.0f && b.index != nvr::kNoIndex)
+            score = nvr::gumbel_score(b.score, temperature, seeds[r], uint32_t(b.index));
+        partial_scores[blockIdx.x] = score;
         partial_ids[blockIdx.x] = b.index;
+    }
+}
+
+// Largest value the Gumbel term -ln(-ln(u)) takes over every u the hash can
+// produce (exhaustive over all 2^23 uniforms with nvr_logf): 16.6355324.
+constexpr float kNoiseMax = 0x1.0a2b24p+4f;
+
+// Upper bound of a token's Gumbel score from its logit: logit * (1/T) is
+// within a few ulp of the correctly rounded logit / T, and the 2^-18
+// relative-plus-absolute margin covers that and the final rounding.
+__device__ __forceinline__ float score_bound(float logit, float inv_t) {
+    const float est = logit * inv_t;
+    return (est + kNoiseMax) + (__builtin_fabsf(est) + 17.0f) * 0x1.0p-18f;
+}
+
+// Second pass, same grid as the first; blocks of greedy rows exit at once.
+// (Striding a grid of eight blocks per CU over the items instead was measured
+// no faster for greedy rows: their cost is the dependent launch itself.)
+//
+// Gumbel rows: exact branch-and-bound over the partition. S0 = the largest
+// partial score of the row is the exact score of a real token (the first pass
+// stored the score of each partition's largest logit; refined blocks overwrite
+// theirs with their best), so a token whose score_bound is below S0 cannot be
+// the row's winner. Partials read while other blocks overwrite them are still
+// scores of real tokens, so the race only changes how much is pruned, never
+// the result. Each wave compacts its own candidates into LDS (ballot + mbcnt,
+// no block barrier) and scores them with every lane busy. The block then
+// overwrites its partial. (A last-block combine through a ticket counter was
+// measured 7x slower: publishing a partial at agent scope writes back and
+// invalidates the L2 of the block's XCD.)
+template <int C>
+__global__ __launch_bounds__(256) void sample_refine(const uint16_t* __restrict__ logits,
+                                                     const float* __restrict__ temps,
+                                                     const uint64_t* __restrict__ seeds,
+                                                     float* __restrict__ partial_scores, int* __restrict__ partial_ids,
+                                                     int vocab, int parts) {
+    constexpr int W = 2048 * C;
+    constexpr int kLaneTokens = 8 * C;
+    __shared__ uint32_t queue[4][kWave * kLaneTokens];
+    const int r = blockIdx.x / parts;
+    const int p = blockIdx.x - r * parts;
+    const float temperature = temps[r];
+    if (!(temperature > 0.0f)) return;
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const uint64_t seed = seeds[r];
+    const int64_t first = int64_t(r) * parts;
+    const int begin = p * W;
+    const int end = int(min(int64_t(begin) + W, int64_t(vocab)));
+    const uint16_t* row = logits + int64_t(r) * vocab;
+
+    // Every wave folds the row's partial scores itself (no block barrier). The
+    // first 64 are loaded before the logits so the fold need not wait for them.
+    float s0 = lane < parts ? __hip_atomic_load(partial_scores + first + lane, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : -__builtin_inff();
+    uint4 w[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int t = begin + 8 * int(threadIdx.x) + 2048 * c;
+        w[c] = t < end ? nvr::load_stream(row + t) : make_uint4(0, 0, 0, 0);
+    }
+    for (int q = lane + kWave; q < parts; q += kWave)
+        s0 = fmaxf(s0, __hip_atomic_load(partial_scores + first + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+#pragma unroll
+    for (int m = kWave / 2; m > 0; m >>= 1) s0 = fmaxf(s0, nvr::xor_lane(s0, m));
+    const float inv_t = 1.0f / temperature;
+
+    // Compaction: entry = token offset in the partition (low 16 bits) | logit
+    // bits (high 16 bits). A wave holds at most kWave * kLaneTokens entries.
+    uint32_t* wq = queue[wave];
+    int n = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const bool live = begin + 8 * int(threadIdx.x) + 2048 * c < end;
+        float f[8];
+        nvr::unpack8(w[c], f);
+        const uint32_t words[4] = {w[c].x, w[c].y, w[c].z, w[c].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const bool take = live && !(score_bound(f[i], inv_t) < s0);
+            const uint64_t ballot = __ballot(take);
+            if (take) {
+                const int pos = n + int(__builtin_amdgcn_mbcnt_hi(uint32_t(ballot >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), 0u)));
+                const uint32_t bits = (i & 1) ? (words[i / 2] >> 16) : (words[i / 2] & 0xffffu);
+                wq[pos] = uint32_t(8 * int(threadIdx.x) + 2048 * c + i) | (bits << 16);
+            }
+            n += __popcll(ballot);
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // Two entries per lane per iteration; an odd tail scores one entry twice.
+    Best best{-__builtin_inff(), nvr::kNoIndex};
+    for (int q = lane; q < n; q += 2 * kWave) {
+        const uint32_t e0 = wq[q];
+        const uint32_t e1 = wq[q + kWave < n ? q + kWave : q];
+        const int ta = begin + int(e0 & 0xffffu), tb = begin + int(e1 & 0xffffu);
+        const float sa = nvr::gumbel_score(nvr::bf16_to_f32(uint16_t(e0 >> 16)), temperature, seed, uint32_t(ta));
+        const float sb = nvr::gumbel_score(nvr::bf16_to_f32(uint16_t(e1 >> 16)), temperature, seed, uint32_t(tb));
+        consider(best, sa, ta);
+        consider(best, sb, tb);
+    }
+    best = block_argmax(best);
+    if (threadIdx.x == 0) {
+        __hip_atomic_store(partial_scores + blockIdx.x, best.score, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(partial_ids + blockIdx.x, best.index, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -241,8 +353,12 @@ int nv_sample_parallel(nv_context* c, const void* logits, const void* temps, con
     if (vector_rows(logits, vocab)) {
         // Never more partitions than the scratch holds (ceil(vocab / 2048)).
         parts = int((int64_t(vocab) + 2048 * kChunksPerLane - 1) / (2048 * kChunksPerLane));
-        hipLaunchKernelGGL(sample_partitions_vec<kChunksPerLane>, dim3(unsigned(int64_t(batch) * parts)), dim3(256), 0,
-                           c->stream, l16, t, s, ps, pi, vocab, parts);
+        const int items = batch * parts;
+        hipLaunchKernelGGL(sample_partitions_vec<kChunksPerLane>, dim3(unsigned(items)), dim3(256), 0, c->stream, l16,
+                           t, s, ps, pi, vocab, parts);
+        NVR_HIP(hipGetLastError());
+        hipLaunchKernelGGL(sample_refine<kChunksPerLane>, dim3(unsigned(items)), dim3(256), 0, c->stream, l16, t, s,
+                           ps, pi, vocab, parts);
     } else {
         parts = int(ref_parts);
         hipLaunchKernelGGL(sample_partitions_generic, dim3(unsigned(int64_t(batch) * parts)), dim3(256), 0, c->stream,

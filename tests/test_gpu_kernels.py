@@ -315,6 +315,38 @@ def test_sampling_special_values(gpu):
         assert_bits_equal(_run_sampler(gpu, rows, temps, seeds, 5, vocab, parallel=False), want)
 
 
+def _noise(temperature, seed, vocab):
+    """Gumbel term of every token: the score of a zero logit."""
+    return np.array([ora.gumbel_score(0.0, temperature, seed, t) for t in range(vocab)], np.float32)
+
+
+def test_sampling_pruning_edges(gpu):
+    """Rows where the Gumbel sampler's pruning bound is tight or useless:
+    scores flattened to within bf16 rounding (every token a candidate, full
+    per-wave queues), extreme temperatures, equal logits, and a planted near
+    tie between the largest logit and the token with the largest noise."""
+    vocab = 3 * 4096 + 8
+    batch = 7
+    rng = np.random.default_rng(170)
+    seeds = np.array([ora.sampling_seed(5, r, 3) for r in range(batch)], np.uint64)
+    temps = np.array([0.6, 1.7, 1e-4, 1e4, 0.6, 0.6, 0.6], np.float32)
+    logits = ora.normal_bf16((batch, vocab), 171, 0.0, 3.0)
+    for r, base in ((0, 6.0), (1, -2.0)):  # logit = base - T * noise: every score ~ base / T
+        logits[r] = bf16_of(np.float32(base) - temps[r] * _noise(float(temps[r]), int(seeds[r]), vocab))
+    logits[4] = bf16_of(np.ones(vocab, np.float32))
+    for r in (5, 6):
+        noise = _noise(float(temps[r]), int(seeds[r]), vocab)
+        m = int(np.argmax(f32_of(logits[r])))
+        j = int(np.argmax(np.where(np.arange(vocab) == m, -np.inf, noise)))
+        lm = f32_of(logits[r, m])
+        target = np.float32(lm - temps[r] * (noise[j] - noise[m]))
+        step = np.float32(0.0) if r == 5 else np.float32(abs(target) * 2**-7)
+        logits[r, j] = bf16_of(target + step)
+    want = ora.sample(logits, temps, seeds, batch, vocab)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab), want)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab, parallel=False), want)
+
+
 def test_sampling_reference_golden_vectors(gpu):
     import os
 

@@ -8,6 +8,7 @@ closed forms in float64, or brute force on small inputs. No GPU needed.
 import json
 import math
 import os
+import re
 
 import numpy as np
 import pytest
@@ -81,6 +82,11 @@ def test_logf_is_faithful_on_the_whole_gumbel_domain():
     # Bounds of the Gumbel noise -ln(-ln u) the sampler can produce.
     assert float(l2.min()) == pytest.approx(-16.6355324, abs=1e-6)
     assert float(l2.max()) == pytest.approx(2.81154084, abs=1e-6)
+    # The GPU sampler prunes tokens with this maximum as the noise bound
+    # (kNoiseMax in csrc/sample.hip); it must not be below the true maximum.
+    src = open(os.path.join(os.path.dirname(__file__), "..", "nano-vllm-rs_amd", "csrc", "sample.hip")).read()
+    bound = float.fromhex(re.search(r"kNoiseMax = (0x[0-9a-fA-Fp.+-]+)f;", src).group(1))
+    assert np.float32(bound) == np.float32(-l2.min())
 
 
 def test_logf_is_faithful_on_random_positive_normals():
