@@ -112,9 +112,13 @@ int nv_qkv_rope_cached(nv_context* c, const void* qkv, const void* qw, const voi
                        int rows, int qh, int kvh, int dim, int bs, int blocks, float eps,
                        const void* rope_cache, int max_positions);
 
-/* kernels/kernels.cu:475-485 — causal paged attention (src/gpu.rs:826-887).
- * Exported so the reference links; outside this library's scope it returns
- * -2 with a message. */
+/* kernels/kernels.cu:475-485 — causal paged GQA attention over flattened
+ * ragged prefill and decode rows (src/gpu.rs:826-887). q, out: [rows, qh, dim]
+ * bf16; kc, vc: [blocks, bs, kvh, dim] bf16; positions, seqs: [rows] i32;
+ * tables: [batch, stride] i32. Row r attends to positions[r] + 1 keys of
+ * sequence seqs[r] in the fp32 order of kernels/kernels.cu:226-346. Returns -2
+ * for qh % kvh != 0, an odd head dim or one above 256, or max_context outside
+ * [1, 4096]. */
 int nv_attention(nv_context* c, const void* q, const void* kc, const void* vc,
                  const void* positions, const void* seqs, const void* tables, void* out,
                  int rows, int qh, int kvh, int dim, int bs, int blocks, int stride, int batch,

@@ -109,6 +109,33 @@ __device__ __forceinline__ float swizzle_xor16(float v) {
 // bare v_sqrt_f32 and is deliberately not used.
 __device__ __forceinline__ float inv_sqrt_rn(float x) { return 1.0f / sqrtf(x); }
 
+// ----------------------------------------------------------- exponential ----
+// e^x with fixed bits on host and device (the oracle's ora_expf performs the
+// same operations). k = rint(x * log2 e); r = x - k*ln2_hi - k*ln2_lo with a
+// 16-bit ln2_hi so k*ln2_hi is exact; e^r by its degree-7 Taylor polynomial on
+// |r| <= 0.35; then 2^k by exponent construction. A result below 2^-126 is
+// formed by one multiplication into the subnormal range (one rounding).
+__device__ __forceinline__ float pow2i(int n) { return __uint_as_float(uint32_t(n + 127) << 23); }  // -126..127
+__device__ __forceinline__ float nvr_expf(float x) {
+    if (!(x >= -110.0f)) return x != x ? x : 0.0f;  // NaN stays NaN; e^x < 2^-158 rounds to 0
+    if (x > 88.75f) return __builtin_inff();
+    const float kf = __builtin_rintf(x * 0x1.715476p+0f);
+    const int k = int(kf);
+    float r = __builtin_fmaf(kf, -0x1.62e400p-1f, x);
+    r = __builtin_fmaf(kf, -0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;            // 1/7!
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);  // 1/6!
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);   // 1/5!
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);   // 1/4!
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);   // 1/3!
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    if (k > 127) return (p * pow2i(k - 1)) * 2.0f;
+    if (k >= -126) return p * pow2i(k);
+    return (p * pow2i(k + 64)) * 0x1.0p-64f;
+}
+
 // ------------------------------------------------------------- logarithm ----
 // ln(x) for positive normal x. x = 2^e * m with m in [sqrt(1/2), sqrt(2));
 // f = m - 1 is exact; ln(1+f) = f + f^2 * Q(f) with Q a degree-8 fit of

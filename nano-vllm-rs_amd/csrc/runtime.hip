@@ -185,12 +185,6 @@ int nv_gemm(nv_context* c, const void* x, const void* w, void* y, int m, int n, 
     return 0;
 }
 
-int nv_attention(nv_context* c, const void*, const void*, const void*, const void*, const void*, const void*,
-                 void*, int, int, int, int, int, int, int, int, int) {
-    NVR_ACTIVATE(c);
-    return nvr::fail(-2, "nv_attention: paged attention is not provided by this library");
-}
-
 uint64_t nv_sampling_seed(uint64_t base, uint64_t request_id, uint64_t generated) {
     auto mix = [](uint64_t v) {
         v += 0x9e3779b97f4a7c15ull;

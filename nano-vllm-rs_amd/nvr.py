@@ -437,6 +437,30 @@ class Gpu:
                                            _dimension(block_size), _dimension(num_blocks), eps, rope_cache.ptr,
                                            _dimension(max_positions)))
 
+    def paged_attention(self, q: Buffer, kcache: Buffer, vcache: Buffer, positions: Buffer, seq_indices: Buffer,
+                        block_tables: Buffer, out: Buffer, rows: int, qheads: int, kvheads: int, head_dim: int,
+                        block_size: int, num_blocks: int, table_stride: int, batch_size: int,
+                        max_context: int) -> None:
+        """Causal paged GQA over flattened ragged prefill and decode rows
+        (src/gpu.rs:826-887). KV layout [blocks, block_size, kvheads, head_dim];
+        each row attends to positions[row] + 1 keys of sequence seq_indices[row]."""
+        self._heads(qheads, kvheads, head_dim)
+        if not 0 < max_context <= 4096:
+            raise ValueError("paged attention supports at most 4096 context tokens")
+        self.tensor(q, [rows, qheads, head_dim], 2)
+        self.tensor(out, [rows, qheads, head_dim], 2)
+        for cache in (kcache, vcache):
+            self.tensor(cache, [num_blocks, block_size, kvheads, head_dim], 2)
+        for meta in (positions, seq_indices):
+            self.tensor(meta, [rows], 4)
+        self.tensor(block_tables, [batch_size, table_stride], 4)
+        self.distinct(out, [q, kcache, vcache, positions, seq_indices, block_tables])
+        _check(self.lib.nv_attention(self.handle, q.ptr, kcache.ptr, vcache.ptr, positions.ptr, seq_indices.ptr,
+                                     block_tables.ptr, out.ptr, _dimension(rows), _dimension(qheads),
+                                     _dimension(kvheads), _dimension(head_dim), _dimension(block_size),
+                                     _dimension(num_blocks), _dimension(table_stride), _dimension(batch_size),
+                                     _dimension(max_context)))
+
     def kv_write(self, k: Buffer, v: Buffer, slots: Buffer, kcache: Buffer, vcache: Buffer, rows: int,
                  kvheads: int, head_dim: int, block_size: int, num_blocks: int) -> None:
         """Standalone paged KV-cache slot write (no counterpart method in src/gpu.rs)."""

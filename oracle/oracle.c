@@ -127,6 +127,36 @@ void ora_logf_n(const float* in, float* out, size_t n) {
     for (size_t i = 0; i < n; ++i) out[i] = ora_logf(in[i]);
 }
 
+/* Stands in for CUDA expf at kernels/kernels.cu:254,320 (attention
+ * probabilities). k = rint(x*log2 e); r = x - k*ln2_hi - k*ln2_lo (ln2_hi has
+ * 16 significant bits, so k*ln2_hi is exact); e^r = degree-7 Taylor polynomial
+ * on |r| <= 0.35; 2^k by exponent construction, with results below 2^-126
+ * formed by one multiplication into the subnormal range. */
+static inline float pow2i(int n) { return u2f((uint32_t)(n + 127) << 23); }
+float ora_expf(float x) {
+    if (!(x >= -110.0f)) return x != x ? x : 0.0f;
+    if (x > 88.75f) return INFINITY;
+    const float kf = rintf(x * 0x1.715476p+0f);
+    const int k = (int)kf;
+    float r = fmaf(kf, -0x1.62e400p-1f, x);
+    r = fmaf(kf, -0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);
+    p = fmaf(p, r, 0x1.111112p-7f);
+    p = fmaf(p, r, 0x1.555556p-5f);
+    p = fmaf(p, r, 0x1.555556p-3f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    if (k > 127) return (p * pow2i(k - 1)) * 2.0f;
+    if (k >= -126) return p * pow2i(k);
+    return (p * pow2i(k + 64)) * 0x1.0p-64f;
+}
+
+void ora_expf_n(const float* in, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) out[i] = ora_expf(in[i]);
+}
+
 /* kernels/kernels.cu:384-388. */
 float ora_gumbel_score(float logit, float temperature, uint64_t seed, uint32_t token) {
     const uint64_t r = ora_splitmix64(seed ^ ((uint64_t)token * 0xd2b74407b1ce6e93ull));
@@ -450,6 +480,96 @@ static void silu_range(void* p, int64_t r0, int64_t r1) {
 void ora_silu(const uint16_t* packed, uint16_t* out, int rows, int intermediate, int threads) {
     struct silu_ctx g = {packed, out, intermediate};
     parallel_for(rows, threads, silu_range, &g);
+}
+
+/* ----------------------------------------------------- paged attention ---- */
+/* kernels/kernels.cu:226-270 (attention_kernel) and :289-346
+ * (attention_ordered_kernel, documented at :286-287 to keep the first one's
+ * fp32 order). Per (row, head), kvhead = head / (qh / kvh):
+ *   - rows with seq outside [0, batch) or context = pos + 1 outside
+ *     [1, max_context] or above stride * bs produce zeros (:231-234, :295-298);
+ *   - token t reads physical block table[seq*stride + t/bs] (:240, :277-284);
+ *     a block outside [0, num_blocks) gives score -inf and no V term;
+ *   - score = warp_sum(chain_0 .. chain_31) * rsqrt(dim), where lane c's chain
+ *     accumulates q[d]*k[d] for d = c, c+32, ... < dim with `dot += q*k`
+ *     (contracted to fma) from 0 (:243-245, :306-312); rsqrt -> 1/sqrtf;
+ *   - m = max of the scores; p_t = exp(score_t - m) when m is finite, else 0
+ *     (:253-254, :319-320); den = block_sum of thread partials, thread i adding
+ *     p_i, p_{i+256}, ... in order (:251-258, :318-324);
+ *   - value_d = sum over tokens in order of p_t * v_t[d] (contracted to fma)
+ *     from 0; out = bf16(den > 0 ? value_d / den : 0) (:260-268, :325-345). */
+struct attn_ctx {
+    const uint16_t *q, *kc, *vc;
+    const int32_t *positions, *seqs, *tables;
+    uint16_t* out;
+    int qh, kvh, dim, bs, blocks, stride, batch, max_context;
+};
+
+static void attention_range(void* p, int64_t i0, int64_t i1) {
+    const struct attn_ctx* a = (const struct attn_ctx*)p;
+    float* scores = (float*)malloc(sizeof(float) * (size_t)(a->max_context > 0 ? a->max_context : 1));
+    const float scale = 1.0f / sqrtf((float)a->dim);
+    for (int64_t i = i0; i < i1; ++i) {
+        const int64_t row = i / a->qh;
+        const int head = (int)(i % a->qh);
+        const int kvhead = head / (a->qh / a->kvh);
+        const uint16_t* q = a->q + i * a->dim;
+        uint16_t* out = a->out + i * a->dim;
+        const int seq = a->seqs[row];
+        const int64_t context = (int64_t)a->positions[row] + 1;
+        if (seq < 0 || seq >= a->batch || context < 1 || context > a->max_context ||
+            context > (int64_t)a->stride * a->bs || scores == NULL) {
+            for (int d = 0; d < a->dim; ++d) out[d] = 0;
+            continue;
+        }
+        const int32_t* table = a->tables + (int64_t)seq * a->stride;
+        float m = -INFINITY;
+        for (int t = 0; t < (int)context; ++t) {
+            const int block = table[t / a->bs];
+            float score = -INFINITY;
+            if (block >= 0 && block < a->blocks) {
+                const uint16_t* k = a->kc + (((int64_t)block * a->bs + t % a->bs) * a->kvh + kvhead) * a->dim;
+                float lane[32];
+                for (int c = 0; c < 32; ++c) {
+                    float dot = 0.0f;
+                    for (int d = c; d < a->dim; d += 32) dot = fmaf(bf(q[d]), bf(k[d]), dot);
+                    lane[c] = dot;
+                }
+                score = warp_sum_lane0(lane) * scale;
+            }
+            scores[t] = score;
+            m = fmaxf(m, score);
+        }
+        float part[256];
+        for (int th = 0; th < 256; ++th) {
+            float sum = 0.0f;
+            for (int t = th; t < (int)context; t += 256) {
+                const float pr = isfinite(m) ? ora_expf(scores[t] - m) : 0.0f;
+                scores[t] = pr;
+                sum += pr;
+            }
+            part[th] = sum;
+        }
+        const float den = block_sum_256(part);
+        for (int d = 0; d < a->dim; ++d) {
+            float value = 0.0f;
+            for (int t = 0; t < (int)context; ++t) {
+                const int block = table[t / a->bs];
+                if (block < 0 || block >= a->blocks) continue;
+                const uint16_t* v = a->vc + (((int64_t)block * a->bs + t % a->bs) * a->kvh + kvhead) * a->dim;
+                value = fmaf(scores[t], bf(v[d]), value);
+            }
+            out[d] = ora_bf16_from_f32(den > 0.0f ? value / den : 0.0f);
+        }
+    }
+    free(scores);
+}
+
+void ora_attention(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const int32_t* positions,
+                   const int32_t* seqs, const int32_t* tables, uint16_t* out, int rows, int qh, int kvh, int dim,
+                   int bs, int blocks, int stride, int batch, int max_context, int threads) {
+    struct attn_ctx a = {q, kc, vc, positions, seqs, tables, out, qh, kvh, dim, bs, blocks, stride, batch, max_context};
+    parallel_for((int64_t)rows * qh, threads, attention_range, &a);
 }
 
 /* --------------------------------------------------------- sampling ---- */

@@ -15,6 +15,7 @@
  *   logf       -> ora_logf (range reduction + degree-8 polynomial, <1 ulp)
  *   powf/sincosf in the RoPE table -> binary64 series, rounded to fp32
  *   expf (SiLU) -> the C library's expf (SiLU is compared within 1 bf16 ulp)
+ *   expf (attention) -> ora_expf (range reduction + degree-7 polynomial)
  *
  * Functions taking `threads` split rows over that many POSIX threads
  * (threads <= 1 runs on the caller's thread); results do not depend on it.
@@ -36,6 +37,8 @@ uint64_t ora_splitmix64(uint64_t v);
 uint64_t ora_sampling_seed(uint64_t base, uint64_t request_id, uint64_t generated);
 float ora_logf(float x);
 void ora_logf_n(const float* in, float* out, size_t n);
+float ora_expf(float x);
+void ora_expf_n(const float* in, float* out, size_t n);
 float ora_gumbel_score(float logit, float temperature, uint64_t seed, uint32_t token);
 void ora_rope_cos_sin(int position, int pair, int dim, float theta, float* c, float* s);
 /* Sum of squares of v[0..n) in the reference's 256-thread block order. */
@@ -65,6 +68,12 @@ void ora_sample(const uint16_t* logits, const float* temps, const uint64_t* seed
  * (nv_sample_parallel uses 2048), partials included. */
 void ora_sample_partitioned(const uint16_t* logits, const float* temps, const uint64_t* seeds, int32_t* out,
                             float* partial_scores, int32_t* partial_ids, int batch, int vocab, int width);
+
+/* Paged causal GQA attention (nv_attention); q, out [rows, qh, dim];
+ * caches [blocks, bs, kvh, dim]; tables [batch, stride]. */
+void ora_attention(const uint16_t* q, const uint16_t* kc, const uint16_t* vc, const int32_t* positions,
+                   const int32_t* seqs, const int32_t* tables, uint16_t* out, int rows, int qh, int kvh, int dim,
+                   int bs, int blocks, int stride, int batch, int max_context, int threads);
 
 /* Deterministic synthetic data: SplitMix64 stream `seed`, Box-Muller in
  * binary64, rounded to bf16. */

@@ -30,6 +30,9 @@ _SIGS = {
     "ora_sampling_seed": (_u64, [_u64, _u64, _u64]),
     "ora_logf": (_f, [_f]),
     "ora_logf_n": (None, [_p, _p, ctypes.c_size_t]),
+    "ora_expf": (_f, [_f]),
+    "ora_expf_n": (None, [_p, _p, ctypes.c_size_t]),
+    "ora_attention": (None, [_p] * 7 + [_i] * 10),
     "ora_gumbel_score": (_f, [_f, _f, _u64, ctypes.c_uint32]),
     "ora_rope_cos_sin": (None, [_i, _i, _i, _f, ctypes.POINTER(_f), ctypes.POINTER(_f)]),
     "ora_block_sum_sq": (_f, [_p, _i]),
@@ -93,6 +96,17 @@ def logf_array(x) -> np.ndarray:
     x = _c(x, np.float32)
     out = np.empty_like(x)
     lib().ora_logf_n(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def expf(x: float) -> float:
+    return lib().ora_expf(x)
+
+
+def expf_array(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    lib().ora_expf_n(x.ctypes.data, out.ctypes.data, x.size)
     return out
 
 
@@ -202,3 +216,14 @@ def sample_partitioned(logits, temps, seeds, batch, vocab, width=2048):
     lib().ora_sample_partitioned(_ptr(logits), _ptr(temps), _ptr(seeds), _ptr(out), _ptr(ps), _ptr(pi), batch,
                                  vocab, width)
     return out, ps, pi
+
+
+def attention(q, kc, vc, positions, seqs, tables, rows, qh, kvh, dim, bs, blocks, stride, batch, max_context,
+              threads=1):
+    """Paged causal GQA attention; returns out [rows, qh, dim] bf16 bits."""
+    q, kc, vc = _c(q, np.uint16), _c(kc, np.uint16), _c(vc, np.uint16)
+    positions, seqs, tables = _c(positions, np.int32), _c(seqs, np.int32), _c(tables, np.int32)
+    out = np.empty((rows, qh, dim), np.uint16)
+    lib().ora_attention(_ptr(q), _ptr(kc), _ptr(vc), _ptr(positions), _ptr(seqs), _ptr(tables), _ptr(out), rows, qh,
+                        kvh, dim, bs, blocks, stride, batch, max_context, threads)
+    return out

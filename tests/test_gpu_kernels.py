@@ -358,6 +358,101 @@ def test_sampling_reference_golden_vectors(gpu):
     assert _run_sampler(gpu, logits, temps, seeds, b, v, parallel=False).tolist() == expected.tolist()
 
 
+# -------------------------------------------------------- paged attention ---
+def _attention(gpu, q, kc, vc, pos, seqs, tables, rows, qh, kvh, dim, bs, blocks, stride, batch, max_context,
+               align=True):
+    put = up if align else misaligned
+    out = gpu.alloc(rows * qh * dim * 2)
+    gpu.paged_attention(put(gpu, q), up(gpu, kc), up(gpu, vc), up(gpu, pos), up(gpu, seqs), up(gpu, tables), out,
+                        rows, qh, kvh, dim, bs, blocks, stride, batch, max_context)
+    return down(out, np.uint16, (rows, qh, dim))
+
+
+def _attention_case(gpu, seed, pos, seqs, qh, kvh, dim, bs, batch, stride, max_context, q_std=1.0, holes=(),
+                    align=True):
+    rows = len(pos)
+    blocks = batch * stride
+    rng = np.random.default_rng(seed)
+    tables = rng.permutation(blocks).astype(np.int32)
+    for i, b in holes:
+        tables[i] = b
+    pos, seqs = np.asarray(pos, np.int32), np.asarray(seqs, np.int32)
+    q = ora.normal_bf16((rows, qh, dim), seed + 1, 0.0, q_std)
+    kc = ora.normal_bf16((blocks, bs, kvh, dim), seed + 2, 0.0, 1.0)
+    vc = ora.normal_bf16((blocks, bs, kvh, dim), seed + 3, 0.0, 1.0)
+    want = ora.attention(q, kc, vc, pos, seqs, tables, rows, qh, kvh, dim, bs, blocks, stride, batch, max_context,
+                         threads=8)
+    got = _attention(gpu, q, kc, vc, pos, seqs, tables, rows, qh, kvh, dim, bs, blocks, stride, batch, max_context,
+                     align)
+    assert_bits_equal(got, want)
+    return want
+
+
+@pytest.mark.parametrize("q_std", [1.0, 6.0])
+def test_attention_decode_qwen3_shapes(gpu, q_std):
+    """16 decode rows of Qwen3-0.6B attention (16 q heads, 8 kv heads, dim 128,
+    256-token blocks) with contexts up to 4096; q_std 6 spreads the scores so
+    many probabilities are subnormal or zero."""
+    rng = np.random.default_rng(200)
+    batch, stride = 16, 16
+    pos = np.r_[4095, 0, 255, 256, rng.integers(0, 4096, size=12)]
+    _attention_case(gpu, 201, pos, np.arange(batch), 16, 8, 128, 256, batch, stride, 4096, q_std=q_std)
+
+
+def test_attention_ragged_prefill_rows(gpu):
+    """Flattened prefill of three sequences (300, 1 and 700 tokens) with
+    16-token blocks, one row per token."""
+    lens = [300, 1, 700]
+    pos = np.concatenate([np.arange(n) for n in lens])
+    seqs = np.concatenate([np.full(n, i) for i, n in enumerate(lens)])
+    _attention_case(gpu, 210, pos, seqs, 16, 8, 128, 16, 3, 44, 1024)
+
+
+@pytest.mark.parametrize("dim,qh,kvh,bs", [(32, 4, 2, 8), (64, 8, 2, 256), (256, 4, 4, 16), (128, 6, 2, 7),
+                                           (128, 4, 4, 32), (80, 4, 2, 16), (96, 2, 1, 5), (2, 2, 2, 4)])
+def test_attention_head_dims_groups_and_block_sizes(gpu, dim, qh, kvh, bs):
+    rng = np.random.default_rng(dim * 7 + bs)
+    batch, max_context = 4, 520
+    stride = -(-max_context // bs)
+    pos = rng.integers(0, max_context, size=9)
+    pos[0] = max_context - 1
+    seqs = rng.integers(0, batch, size=9)
+    _attention_case(gpu, 220 + dim, pos, seqs, qh, kvh, dim, bs, batch, stride, max_context)
+
+
+def test_attention_invalid_rows_and_blocks(gpu):
+    """Rows with a bad sequence index or a context beyond max_context or the
+    table give zeros; table entries outside [0, blocks) drop their tokens."""
+    batch, stride, bs = 3, 4, 64
+    pos = [100, 0, 255, 300, 200, 63, 64, 10]
+    seqs = [0, -1, 1, 0, 3, 2, 2, 1]
+    holes = [(1, -1), (stride + 0, 3 * stride + 9), (2 * stride + 1, -7)]
+    want = _attention_case(gpu, 230, pos, seqs, 4, 2, 128, bs, batch, stride, 256, holes=holes)
+    assert not want[1].any() and not want[3].any() and not want[4].any()
+
+
+def test_attention_generic_path_for_unaligned_queries(gpu):
+    _attention_case(gpu, 240, [0, 77, 399], [0, 1, 1], 4, 2, 128, 16, 2, 25, 400, align=False)
+
+
+def test_attention_special_values(gpu):
+    """An infinite score (maximum not finite) zeroes the row; NaN keys give NaN
+    scores that the maximum ignores."""
+    dim, bs, blocks = 32, 4, 2
+    q = bf16_of(np.r_[np.full(dim, 3e38), np.ones(dim), np.ones(dim)].astype(np.float32))
+    kc = bf16_of(np.ones((blocks, bs, 1, dim), np.float32))
+    kc2 = kc.copy()
+    kc2[0, 1, 0, 5] = bf16_of(np.float32(np.nan))
+    tables = np.array([0, 1], np.int32)
+    vc = ora.normal_bf16((blocks, bs, 1, dim), 250, 0.0, 1.0)
+    pos, seqs = np.array([5, 5, 2], np.int32), np.zeros(3, np.int32)
+    for keys in (kc, kc2):
+        want = ora.attention(q, keys, vc, pos, seqs, tables, 3, 1, 1, dim, bs, blocks, 2, 1, 8)
+        got = _attention(gpu, q, keys, vc, pos, seqs, tables, 3, 1, 1, dim, bs, blocks, 2, 1, 8)
+        assert_bits_equal(got, want)
+        assert not want[0].any()
+
+
 # ------------------------------------------------------------------- GEMM ----
 def test_gemm_known_answer_and_random(gpu):
     # src/gpu.rs:1290-1298: X = [[1,2,3],[4,5,6]], W = [[1,0,1],[0,1,0]] -> [[4,2],[10,5]].

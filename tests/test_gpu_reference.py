@@ -2,9 +2,6 @@
 library through the same wrapper API (nvr.Gpu mirrors src/gpu.rs), plus graph
 capture/replay of the fused kernels.
 
-Attention (gpu_causal_paged_attention_and_rope's first half,
-gpu_ragged_gqa_matches_cpu) is outside this library; nv_attention reports an
-error instead, which is checked here.
 """
 import math
 
@@ -151,11 +148,81 @@ def test_gpu_rope_known_answers_and_v_slot_write():
     assert values(v, 4 * dim)[0] == 1.0
 
 
-def test_gpu_attention_is_reported_unavailable():
+def test_gpu_causal_paged_attention_known_answer():
+    """First half of src/gpu.rs:1330-1380: zero queries over reversed physical
+    blocks holding V rows 1, 2, 3 give the running means 1, 1.5, 2."""
     gpu = nvr.Gpu(0)
-    code = gpu.lib.nv_attention(gpu.handle, *([None] * 7), 1, 1, 1, 32, 2, 2, 2, 1, 4)
-    assert code == -2
-    assert b"not provided" in gpu.lib.nv_last_error()
+    rows, dim, qh, kvh = 3, 32, 2, 1
+    q = gpu.alloc(rows * qh * dim * 2)
+    k = gpu.alloc(2 * 2 * kvh * dim * 2)
+    cache = np.zeros(4 * dim, np.float32)
+    cache[2 * dim:3 * dim] = 1.0
+    cache[3 * dim:4 * dim] = 2.0
+    cache[:dim] = 3.0
+    v = gpu.upload_array(bf16_of(cache))
+    positions = gpu.upload_array(np.array([0, 1, 2], np.int32))
+    seqs = gpu.upload_array(np.array([0, 0, 0], np.int32))
+    tables = gpu.upload_array(np.array([1, 0], np.int32))
+    out = gpu.alloc(rows * qh * dim * 2)
+    gpu.paged_attention(q, k, v, positions, seqs, tables, out, rows, qh, kvh, dim, 2, 2, 2, 1, 4)
+    actual = values(out, rows * qh * dim)
+    for r in range(rows):
+        assert actual[r * qh * dim:(r + 1) * qh * dim] == [1.0 + 0.5 * r] * (qh * dim)
+
+
+@pytest.mark.parametrize("dim,block_size,pos,seq,table", [
+    (32, 2, [0, 2, 1, 0], [0, 0, 1, 2], [3, 1, 0, 2, 2, -1]),
+    (128, 256, [0, 255, 256, 510], [0, 0, 1, 1], [3, 1, 0, 2]),
+])
+def test_gpu_ragged_gqa_matches_cpu(dim, block_size, pos, seq, table):
+    """src/gpu.rs:1382-1470: ragged GQA rows against the reference test's own
+    f32 formula (tolerance 0.004), and bit for bit against the oracle."""
+    gpu = nvr.Gpu(0)
+    rows, qheads, kvheads, blocks = 4, 4, 2, 4
+    query = ((np.arange(rows * qheads * dim) * 7 % 19) - 9.0) * 0.125
+    key = ((np.arange(blocks * block_size * kvheads * dim) * 11 % 23) - 11.0) * 0.125
+    value = ((np.arange(key.size) * 3 % 13) - 6.0) * 0.125
+    qb, kb, vb = bf16_of(query), bf16_of(key), bf16_of(value)
+    pos_a, seq_a, table_a = (np.array(x, np.int32) for x in (pos, seq, table))
+    out = gpu.alloc(qb.nbytes)
+    gpu.paged_attention(gpu.upload_array(qb), gpu.upload_array(kb), gpu.upload_array(vb), gpu.upload_array(pos_a),
+                        gpu.upload_array(seq_a), gpu.upload_array(table_a), out, rows, qheads, kvheads, dim,
+                        block_size, blocks, 2, len(table) // 2, max(pos) + 1)
+    got = out.download(np.uint16, qb.size)
+    actual = f32_of(got)
+    q32, k32, v32 = query.astype(np.float32), key.astype(np.float32), value.astype(np.float32)
+    for row in range(rows):
+        context = pos[row] + 1
+        for head in range(qheads):
+            kvhead = head // (qheads // kvheads)
+            qbase = (row * qheads + head) * dim
+
+            def base(t):
+                return ((table[seq[row] * 2 + t // block_size] * block_size + t % block_size) * kvheads
+                        + kvhead) * dim
+
+            scores = np.array([np.sum(q32[qbase:qbase + dim] * k32[base(t):base(t) + dim], dtype=np.float32)
+                               / np.float32(math.sqrt(dim)) for t in range(context)], np.float32)
+            probs = np.exp(scores - scores.max()).astype(np.float32)
+            total = probs.sum(dtype=np.float32)
+            for d in range(dim):
+                expected = sum(float(probs[t]) * float(v32[base(t) + d]) for t in range(context)) / float(total)
+                assert abs(actual[qbase + d] - expected) < 0.004, (row, head, d)
+    want = ora.attention(qb, kb, vb, pos_a, seq_a, table_a, rows, qheads, kvheads, dim, block_size, blocks, 2,
+                         len(table) // 2, max(pos) + 1)
+    assert np.array_equal(got, want.reshape(-1))
+
+
+def test_gpu_attention_rejects_unsupported_arguments():
+    gpu = nvr.Gpu(0)
+    lib, h = gpu.lib, gpu.handle
+    assert lib.nv_attention(h, *([None] * 7), 1, 2, 1, 32, 2, 2, 2, 1, 4097) == -2
+    assert b"max_context" in lib.nv_last_error()
+    assert lib.nv_attention(h, *([None] * 7), 1, 3, 2, 32, 2, 2, 2, 1, 4) == -2
+    assert lib.nv_attention(h, *([None] * 7), 1, 2, 1, 33, 2, 2, 2, 1, 4) == -2
+    assert lib.nv_attention(h, *([None] * 7), 0, 2, 1, 32, 2, 2, 2, 1, 4) == -2
+    with pytest.raises(ValueError):
+        gpu.paged_attention(*([gpu.alloc(64)] * 7), 1, 2, 1, 32, 2, 2, 2, 1, 4097)
 
 
 def test_gpu_alloc_is_zero_filled_and_errors_carry_messages():

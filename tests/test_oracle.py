@@ -352,3 +352,100 @@ def test_sampling_edge_rows():
     temps[:] = 0.7
     out = ora.sample(rows, temps, seeds, 4, vocab)
     assert out[0] == 0 and out[2] == 77
+
+
+# ---------------------------------------------------------- exponential -----
+def test_expf_is_faithful_on_the_attention_domain():
+    """exp(x) for x <= 0 (scores minus their maximum), subnormal results
+    included, within one ulp of binary64 exp; special values."""
+    rng = np.random.default_rng(3)
+    bits = rng.integers(0x80000000, 0xC2DC0000, size=3_000_000, dtype=np.uint64).astype(np.uint32)
+    x = np.concatenate([bits.view(np.float32), -np.linspace(0, 110, 1_000_001, dtype=np.float32),
+                        np.linspace(0, 88.7, 100_001, dtype=np.float32)])
+    got = ora.expf_array(x).astype(np.float64)
+    want = np.exp(x.astype(np.float64))
+    spacing = np.maximum(np.spacing(np.abs(want.astype(np.float32))).astype(np.float64), 2.0**-149)
+    assert (np.abs(got - want) / spacing).max() < 1.0
+    assert ora.expf(0.0) == 1.0
+    assert ora.expf(float("-inf")) == 0.0
+    assert math.isnan(ora.expf(float("nan")))
+    assert ora.expf(-120.0) == 0.0 and ora.expf(100.0) == float("inf")
+
+
+# ----------------------------------------------------- paged attention -----
+def attention_f64(q, kc, vc, pos, seqs, tables, qh, kvh, dim, bs, blocks, stride, batch, max_context):
+    """Softmax attention in binary64 from the contract of
+    kernels/kernels.cu:226-270 (no fp32 rounding order)."""
+    rows = len(pos)
+    qf, kf, vf = (f32_of(a).astype(np.float64) for a in (q, kc, vc))
+    qf = qf.reshape(rows, qh, dim)
+    kf = kf.reshape(blocks, bs, kvh, dim)
+    vf = vf.reshape(blocks, bs, kvh, dim)
+    out = np.zeros((rows, qh, dim))
+    for r in range(rows):
+        ctx = int(pos[r]) + 1
+        if not (0 <= seqs[r] < batch) or ctx < 1 or ctx > max_context or ctx > stride * bs:
+            continue
+        ks, vs = [], []
+        for t in range(ctx):
+            b = int(tables[seqs[r] * stride + t // bs])
+            if 0 <= b < blocks:
+                ks.append(kf[b, t % bs])
+                vs.append(vf[b, t % bs])
+        if not ks:
+            continue
+        K, V = np.stack(ks), np.stack(vs)
+        for h in range(qh):
+            s = K[:, h // (qh // kvh)] @ qf[r, h] / math.sqrt(dim)
+            p = np.exp(s - s.max())
+            out[r, h] = p @ V[:, h // (qh // kvh)] / p.sum()
+    return out
+
+
+def test_attention_known_answers():
+    # src/gpu.rs:1330-1362: zero queries, reversed blocks holding V rows 1, 2, 3.
+    dim = 32
+    v = np.zeros(4 * dim, np.float32)
+    v[2 * dim:3 * dim], v[3 * dim:], v[:dim] = 1.0, 2.0, 3.0
+    out = ora.attention(np.zeros(3 * 2 * dim, np.uint16), np.zeros(4 * dim, np.uint16), bf16_of(v),
+                        np.array([0, 1, 2], np.int32), np.zeros(3, np.int32), np.array([1, 0], np.int32),
+                        3, 2, 1, dim, 2, 2, 2, 1, 4)
+    for r in range(3):
+        assert np.all(f32_of(out[r]) == 1.0 + 0.5 * r)
+    # One key: p = 1, den = 1, the output is that key's V row exactly.
+    rng = np.random.default_rng(4)
+    vrow = bf16_of(rng.normal(size=(1, 1, 1, 64)).astype(np.float32))
+    q = bf16_of(rng.normal(size=(1, 1, 64)).astype(np.float32))
+    k = bf16_of(rng.normal(size=(1, 1, 1, 64)).astype(np.float32))
+    out = ora.attention(q, k, vrow, np.array([0], np.int32), np.array([0], np.int32), np.array([0], np.int32),
+                        1, 1, 1, 64, 1, 1, 1, 1, 1)
+    assert np.array_equal(out.reshape(-1), vrow.reshape(-1))
+    # Equal scores over a constant V column: the mean is the constant exactly.
+    vconst = bf16_of(np.tile(np.linspace(-2, 2, 32, dtype=np.float32), 8 * 4))
+    out = ora.attention(np.zeros(32, np.uint16), np.zeros(8 * 4 * 32, np.uint16), vconst,
+                        np.array([29], np.int32), np.array([0], np.int32), np.arange(4, dtype=np.int32),
+                        1, 1, 1, 32, 8, 4, 4, 1, 30)
+    assert np.array_equal(out.reshape(-1), vconst[:32])
+
+
+@pytest.mark.parametrize("dim,bs,qh,kvh", [(128, 256, 16, 8), (64, 16, 4, 1), (80, 3, 6, 2), (32, 2, 3, 3)])
+def test_attention_matches_float64_softmax(dim, bs, qh, kvh):
+    """Random ragged rows, invalid rows and invalid table entries against the
+    binary64 formula; GQA head mapping included."""
+    rng = np.random.default_rng(dim + bs)
+    batch, stride = 3, -(-600 // bs)
+    blocks = batch * stride
+    tables = rng.permutation(blocks).astype(np.int32)
+    tables[stride + 1] = -1          # a hole in sequence 1
+    tables[2 * stride] = blocks + 5  # an out-of-range block in sequence 2
+    pos = np.array([0, 5, 599, 300, 17, 4096, 42, 599], np.int32)
+    seqs = np.array([0, 1, 2, 1, 0, 0, 7, -1], np.int32)
+    rows, max_context = len(pos), 600
+    q = ora.normal_bf16((rows, qh, dim), 11 + dim, 0.0, 1.0)
+    kc = ora.normal_bf16((blocks, bs, kvh, dim), 12 + dim, 0.0, 1.0)
+    vc = ora.normal_bf16((blocks, bs, kvh, dim), 13 + dim, 0.0, 1.0)
+    got = f32_of(ora.attention(q, kc, vc, pos, seqs, tables, rows, qh, kvh, dim, bs, blocks, stride, batch,
+                               max_context, threads=4)).astype(np.float64)
+    want = attention_f64(q, kc, vc, pos, seqs, tables, qh, kvh, dim, bs, blocks, stride, batch, max_context)
+    assert np.all(np.abs(got - want) <= 2.0**-8 * np.abs(want) + 2.0**-16)
+    assert np.all(got[5:] == 0.0)  # context above max_context, seq out of range, negative seq
