@@ -156,6 +156,12 @@ def bytes_kv_write(rows):
     return rows * 4 + 2 * 2 * rows * KVH * D * 2
 
 
+def bytes_attention(rows, context, table_stride):
+    """K and V rows of every context token of each (row, kv head), q, out and
+    the row's metadata."""
+    return rows * (2 * context * KVH * D * 2 + 2 * QH * D * 2 + 8 + table_stride * 4)
+
+
 def bytes_sampling(batch, vocab):
     return batch * vocab * 2 + batch * (4 + 8 + 4)
 
@@ -320,6 +326,25 @@ def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain, only=()):
                                                                    blocks) for i in range(s)],
                       bytes_kv_write(T), T))
 
+    # Paged attention, decode: 64 sequences at context 4096 (one query row each).
+    if want("attention_decode_64x4096"):
+        B, ctx = 64, MAX_POS
+        stride = ctx // BS
+        blocks = B * stride
+        kc = fill.normal(blocks * BS * KVH * D * 2)
+        vc = fill.normal(blocks * BS * KVH * D * 2)
+        rng = np.random.default_rng(11)
+        tables = fill.ints(rng.permutation(blocks).astype(np.int32))
+        pos = fill.ints(np.full(B, ctx - 1, np.int32))
+        seqs = fill.ints(np.arange(B, dtype=np.int32))
+        qs = [fill.normal(B * QH * D * 2) for _ in range(4)]
+        outs = [gpu.alloc(B * QH * D * 2) for _ in range(4)]
+        cases.append(("attention_decode_64x4096", "paged GQA attention, 64 decode rows x 4096 context, 16/8 heads, "
+                      "dim 128, 256-token blocks (K+V 1.07 GB per launch)",
+                      [lambda i=i: gpu.paged_attention(qs[i], kc, vc, pos, seqs, tables, outs[i], B, QH, KVH, D, BS,
+                                                       blocks, stride, B, ctx) for i in range(4)],
+                      bytes_attention(B, ctx, stride), B))
+
     # Sampling 256 x 151936: rows 0-127 greedy, 128-255 Gumbel at T=0.6.
     if not want("sampling_256x151936", "sampling_greedy", "sampling_gumbel"):
         return cases
@@ -445,9 +470,9 @@ def main() -> int:
 
     # Dominant kernel of the step: largest launches x time at the step's shape.
     roofline = None
-    if kernels:
-        shape_of = {"add_rms": "add_rms_8192x1024", "qkv_rope_cached": "qkv_rope_8192", "silu": "silu_8192x6144"}
-        share = {k: chain.launches()[k] * kernels[v]["us"] for k, v in shape_of.items() if v in kernels}
+    shape_of = {"add_rms": "add_rms_8192x1024", "qkv_rope_cached": "qkv_rope_8192", "silu": "silu_8192x6144"}
+    share = {k: chain.launches()[k] * kernels[v]["us"] for k, v in shape_of.items() if v in kernels}
+    if share:
         dom = max(share, key=share.get)
         kd = kernels[shape_of[dom]]
         roofline = {"kernel": shape_of[dom], "bound": "hbm", "achieved": kd["GB/s"], "peak": HBM_PEAK_GBS,

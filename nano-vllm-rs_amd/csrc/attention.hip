@@ -23,21 +23,25 @@
 //
 // Layout (head dims 32, 64, 128, 256 with 16-byte aligned operands): one
 // 256-thread block per (row, group of HPB q heads sharing a kv head), so a
-// row's K and V are read once for both heads of a GQA pair.
-//   1. Scores: four lanes per token. Lane a of a quad owns chains 8a .. 8a+7,
-//      so it loads k[32j + 8a .. 32j + 8a + 7] (one 16-byte load per j) and q
-//      the same way. The first two tree levels (offsets 16 and 8) pair lanes
-//      a ^ 2 and a ^ 1 of the quad (DPP adds); the last three run inside the
-//      lane. 64 tokens per block step; the next step's K and the step after
-//      that's block-table entries are in flight during the current step.
-//      Scores go to LDS.
+// row's K and V are read once for both heads of a GQA pair. The row's block
+// table is copied to LDS first, so cache addresses never wait on global loads.
+// Every K/V load instruction reads whole token rows (16 lanes per 256-byte
+// row): on MI355X that streams at ~6.6 TB/s, against ~5.2 TB/s when each
+// instruction touches half lines of 16 rows.
+//   1. Scores: four lanes per token. Lane a of a quad owns chains 8a .. 8a+7
+//      (pieces 4j + a of the row, j < dim/32), reached by staging each wave's
+//      16 rows in its own LDS rows (no block barrier). The first two tree
+//      levels (offsets 16 and 8) pair lanes a ^ 2 and a ^ 1 of the quad (DPP
+//      adds); the last three run inside the lane. Three steps of K loads stay
+//      in flight behind the one being scored. Scores go to LDS.
 //   2. Block max, exp in place, the block sum in the reference's order.
-//   3. Values: V tiles of kVTile tokens are staged in LDS with 16-byte loads
-//      (the next tile's loads in flight during the current tile); thread
+//   3. Values: 16 KB V tiles alternate between two LDS slots, one block
+//      barrier per tile; two more tiles are in flight in registers. Thread
 //      (g, d) runs its fma chain over the tile's tokens in order. Tokens of an
 //      invalid block are staged as -0.0 with p = +0, which leaves every chain
 //      value (including -0) unchanged, exactly as skipping them does.
-// Other head dims use a direct kernel with the same arithmetic.
+// Other head dims, unaligned operands and caches of more than 2^31 token rows
+// use a direct kernel with the same arithmetic.
 #include "../../include/nano_hip.h"
 #include "nvr_device.h"
 #include "nvr_internal.h"
@@ -48,7 +52,6 @@ using nvr::kWave;
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kMaxContext = 4096;  // src/gpu.rs:848-852
-constexpr int kVTile = 64;         // tokens per staged V tile
 constexpr uint32_t kNegZeroPair = 0x80008000u;
 
 // 32-lane shuffle-down fold of the reference's warp_sum, valid in lanes 0 and
@@ -75,23 +78,40 @@ __device__ __forceinline__ int64_t phys_token(int entry, int t, int bs, int bloc
     return entry >= 0 && entry < blocks ? int64_t(entry) * bs + t % bs : int64_t(-1);
 }
 
+// Compile-time geometry of attention_ordered.
 template <int DIM, int HPB>
+struct OrderedLayout {
+    static_assert(DIM % 32 == 0 && DIM <= 256 && HPB * DIM <= kThreads, "shape");
+    static constexpr int P = DIM / 32;                    // elements per dot chain
+    static constexpr int kPieces = DIM / 8;               // 16-byte pieces per K/V row
+    static constexpr int kRowsPerLoad = kWave / kPieces;  // whole rows per wave load instruction
+    static constexpr int kQuads = kWave / 4;              // tokens per wave per phase-1 step
+    static constexpr int kStep = kQuads * kWaves;         // tokens per block step
+    static constexpr int kKLoads = kQuads / kRowsPerLoad; // load instructions per wave step (= P)
+    static constexpr int kKRow = DIM * 2 + 64;            // staged K row bytes; the pad makes quad reads conflict-free
+    static constexpr int kVTile = 8192 / DIM;             // tokens per V tile (16 KB)
+    static constexpr int kVLoads = kVTile * kPieces / kThreads;  // V loads per thread per tile (4)
+    static constexpr int kKStage = kWaves * kQuads * kKRow;
+    static constexpr int kVStage = 2 * kVTile * DIM * 2;
+    static constexpr int kStageBytes = kKStage > kVStage ? kKStage : kVStage;
+    static_assert(kKLoads * kRowsPerLoad == kQuads && kVLoads * kThreads == kVTile * kPieces, "tiles");
+};
+
+template <int DIM, int HPB, bool POW2>
 __global__ __launch_bounds__(kThreads) void attention_ordered(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const int* __restrict__ positions, const int* __restrict__ seqs, const int* __restrict__ tables,
-    uint16_t* __restrict__ out, int qh, int kvh, int bs, int blocks, int stride, int batch, int max_context,
-    int score_stride) {
-    static_assert(DIM % 32 == 0 && DIM <= 256 && HPB * DIM <= kThreads, "shape");
-    constexpr int P = DIM / 32;            // elements per chain
-    constexpr int kQuads = kWave / 4;      // tokens per wave per step
-    constexpr int kStep = kQuads * kWaves;  // tokens per block step
-    constexpr int kPieces = DIM / 8;       // 16-byte pieces per K/V row
-    constexpr int kTileLoads = kVTile * kPieces / kThreads;  // per thread
-    static_assert(kTileLoads * kThreads == kVTile * kPieces, "tile");
+    uint16_t* __restrict__ out, int qh, int kvh, int bs, int bs_shift, int blocks, int stride, int batch,
+    int max_context, int score_stride) {
+    using L = OrderedLayout<DIM, HPB>;
+    constexpr int P = L::P, kPieces = L::kPieces, kQuads = L::kQuads, kStep = L::kStep;
+    constexpr int kRowsPerLoad = L::kRowsPerLoad, kKLoads = L::kKLoads, kKRow = L::kKRow;
+    constexpr int kVTile = L::kVTile, kVLoads = L::kVLoads;
 
     extern __shared__ __align__(16) unsigned char smem[];
-    float* probs = reinterpret_cast<float*>(smem);  // [HPB][score_stride]
-    uint16_t* vtile = reinterpret_cast<uint16_t*>(smem + sizeof(float) * HPB * score_stride);  // [kVTile][DIM]
+    float* probs = reinterpret_cast<float*>(smem);                          // [HPB][score_stride]
+    unsigned char* stage = smem + sizeof(float) * HPB * score_stride;       // K rows (phase 1) / V slots (phase 3)
+    int* ltable = reinterpret_cast<int*>(stage + L::kStageBytes);           // the row's block-table entries
     __shared__ float red_max[HPB][kWaves];
     __shared__ float red_sum[HPB][2 * kWaves];
 
@@ -107,13 +127,37 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
         return;
     }
     const int ctx = int(context64);
-    const int* table = tables + int64_t(seq) * stride;
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    const int a = lane & 3;
-    const int64_t token_stride = int64_t(kvh) * DIM;  // elements between tokens of a block
-    const uint16_t* kcol = kc + int64_t(kvhead) * DIM + 8 * a;
+    const int64_t token_stride = int64_t(kvh) * DIM;  // elements between consecutive tokens of a block
+    // The row's block-table entries go to LDS once, so K/V addresses depend on
+    // LDS reads only and the global loads can stay queued.
+    {
+        const int* table = tables + int64_t(seq) * stride;
+        const int nent = (ctx - 1) / bs + 1;
+        for (int i = threadIdx.x; i < nent; i += kThreads) ltable[i] = table[i];
+        __syncthreads();
+    }
+    // Physical token row (block * bs + offset) of logical token t < ctx, or -1
+    // for an invalid block. The host guarantees blocks * bs fits in int32, and
+    // POW2 (bs a power of two) turns the division into a shift.
+    auto phys = [&](int t) -> int {
+        const int lb = POW2 ? t >> bs_shift : t / bs;
+        const int off = POW2 ? t & (bs - 1) : t - lb * bs;
+        const int e = ltable[lb];
+        return e >= 0 && e < blocks ? e * bs + off : -1;
+    };
 
     // ---- 1. scores ----
+    // Loads read whole rows: load instruction k of a wave step gives lane l
+    // 16-byte piece l % kPieces of token k * kRowsPerLoad + l / kPieces (full
+    // 128-byte lines per instruction, which streams markedly faster than
+    // partial lines). The wave stages its kQuads rows in its own LDS rows and
+    // reads them back in the quad layout: lane (tq, a) of quad tq owns chains
+    // 8a .. 8a+7, i.e. pieces 4j + a (j < P) of token tq.
+    const int tq = lane >> 2, a = lane & 3;
+    const int lrow = lane / kPieces, lpiece = lane % kPieces;
+    unsigned char* krows = stage + wave * kQuads * kKRow;
+    const uint16_t* kcol = kc + int64_t(kvhead) * DIM + 8 * lpiece;
     float qf[HPB][P][8];
 #pragma unroll
     for (int g = 0; g < HPB; ++g)
@@ -122,31 +166,40 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
             nvr::unpack8(*reinterpret_cast<const uint4*>(q + (int64_t(row) * qh + h0 + g) * DIM + 32 * j + 8 * a),
                          qf[g][j]);
     const float kScale = 1.0f / sqrtf(float(DIM));
-
-    int tc = wave * kQuads + (lane >> 2);  // this quad's token in the current step
-    int64_t pc = tc < ctx ? phys_token(table[tc / bs], tc, bs, blocks) : -1;
-    uint4 kcur[P];
-#pragma unroll
-    for (int j = 0; j < P; ++j)
-        kcur[j] = pc >= 0 ? nvr::load_stream(kcol + pc * token_stride + 32 * j) : make_uint4(0, 0, 0, 0);
-    int tn = tc + kStep;
-    int entry_n = tn < ctx ? table[tn / bs] : -1;
     float m[HPB];
 #pragma unroll
     for (int g = 0; g < HPB; ++g) m[g] = -__builtin_inff();
 
-    for (int t0 = 0; t0 < ctx; t0 += kStep) {
-        const int64_t pn = tn < ctx ? phys_token(entry_n, tn, bs, blocks) : -1;
-        uint4 knext[P];
+    // Step s covers tokens [s * kStep, (s + 1) * kStep); wave w takes
+    // s * kStep + w * kQuads + (0 .. kQuads - 1). Four K buffers in fixed roles
+    // keep three steps of loads in flight behind the one being scored. Loads
+    // are unconditional (a token past the context or in an invalid block reads
+    // token 0 of block 0 and its dot is discarded), so no branch makes the
+    // compiler drain the load queue.
+    auto issue = [&](uint4 (&kb)[kKLoads], int s) {
 #pragma unroll
-        for (int j = 0; j < P; ++j)
-            knext[j] = pn >= 0 ? nvr::load_stream(kcol + pn * token_stride + 32 * j) : make_uint4(0, 0, 0, 0);
-        const int tnn = tn + kStep;
-        const int entry_nn = tnn < ctx ? table[tnn / bs] : -1;
-
+        for (int k = 0; k < kKLoads; ++k) {
+            const int t = s * kStep + wave * kQuads + k * kRowsPerLoad + lrow;
+            const int ph = phys(min(t, ctx - 1));
+            kb[k] = nvr::load_stream(kcol + int64_t(t < ctx && ph >= 0 ? ph : 0) * token_stride);
+        }
+    };
+    auto score = [&](const uint4 (&kb)[kKLoads], int s) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // the previous step's reads are done
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int k = 0; k < kKLoads; ++k)
+            *reinterpret_cast<uint4*>(krows + (k * kRowsPerLoad + lrow) * kKRow + 16 * lpiece) = kb[k];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         float kf[P][8];
 #pragma unroll
-        for (int j = 0; j < P; ++j) nvr::unpack8(kcur[j], kf[j]);
+        for (int j = 0; j < P; ++j)
+            nvr::unpack8(*reinterpret_cast<const uint4*>(krows + tq * kKRow + 16 * (4 * j + a)), kf[j]);
+        const int t = s * kStep + wave * kQuads + tq;
+        const bool live = t < ctx;
+        const bool valid = live && phys(min(t, ctx - 1)) >= 0;
 #pragma unroll
         for (int g = 0; g < HPB; ++g) {
             float acc[8];
@@ -161,20 +214,54 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
             for (int i = 0; i < 8; ++i) acc[i] += nvr::dpp<nvr::kDppQuadXor2>(acc[i]);
 #pragma unroll
             for (int i = 0; i < 8; ++i) acc[i] += nvr::dpp<nvr::kDppQuadXor1>(acc[i]);
-            const float dot = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
-            const float score = pc >= 0 ? dot * kScale : -__builtin_inff();
-            if (tc < ctx) {
-                m[g] = fmaxf(m[g], score);
-                if (a == 0) probs[g * score_stride + tc] = score;
-            }
+            float dot = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+            // Pin the tree before any branch: the compiler would otherwise sink it
+            // under `valid`, where the DPP operands cannot be fused into their adds.
+            __asm__ volatile("" : "+v"(dot));
+            const float sc = valid ? dot * kScale : -__builtin_inff();
+            m[g] = fmaxf(m[g], live ? sc : -__builtin_inff());
+            if (live && a == 0) probs[g * score_stride + t] = sc;
         }
-#pragma unroll
-        for (int j = 0; j < P; ++j) kcur[j] = knext[j];
-        pc = pn;
-        tc = tn;
-        tn = tnn;
-        entry_n = entry_nn;
+    };
+    const int nsteps = (ctx + kStep - 1) / kStep;
+    {
+        uint4 kA[kKLoads], kB[kKLoads], kC[kKLoads], kD[kKLoads];
+        issue(kA, 0);
+        issue(kB, 1);
+        issue(kC, 2);
+        for (int s = 0; s < nsteps; s += 4) {
+            issue(kD, s + 3);
+            score(kA, s);
+            issue(kA, s + 4);
+            if (s + 1 < nsteps) score(kB, s + 1);
+            issue(kB, s + 5);
+            if (s + 2 < nsteps) score(kC, s + 2);
+            issue(kC, s + 6);
+            if (s + 3 < nsteps) score(kD, s + 3);
+        }
     }
+
+    // ---- V prefetch (see phase 3) ----
+    // A V tile is kVTile whole token rows, 16 KB: load u of thread tid covers
+    // piece cc % kPieces of token cc / kPieces, cc = tid + 256 u. Loads are
+    // unconditional; invalid tokens become -0.0 when staged, which with p = +0
+    // leaves every chain value unchanged, exactly as skipping them does.
+    const uint16_t* vcol = vc + int64_t(kvhead) * DIM;
+    auto load_vtile = [&](uint4 (&r)[kVLoads], bool (&ok)[kVLoads], int t0) {
+#pragma unroll
+        for (int u = 0; u < kVLoads; ++u) {
+            const int cc = int(threadIdx.x) + kThreads * u;
+            const int t = t0 + cc / kPieces;
+            const int ph = phys(min(t, ctx - 1));
+            ok[u] = t < ctx && ph >= 0;
+            r[u] = nvr::load_stream(vcol + int64_t(ok[u] ? ph : 0) * token_stride + 8 * (cc % kPieces));
+        }
+    };
+    bool okW[kVLoads], okX[kVLoads], okY[kVLoads];
+    uint4 rW[kVLoads], rX[kVLoads], rY[kVLoads];
+    load_vtile(rW, okW, 0);
+    load_vtile(rX, okX, kVTile);
+    load_vtile(rY, okY, 2 * kVTile);
 
     // ---- 2. max, exp, block sum ----
 #pragma unroll
@@ -202,70 +289,63 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     for (int g = 0; g < HPB; ++g) den[g] = fold8(red_sum[g]);
 
     // ---- 3. values ----
+    // Thread (g, d) runs the fma chain of head g, dimension d. Tiles alternate
+    // between two LDS slots; one block barrier per tile both publishes the tile
+    // and guarantees the slot written next was consumed by every wave.
     const int g = threadIdx.x / DIM, d = threadIdx.x - g * DIM;
     const bool chain = threadIdx.x < HPB * DIM;
     const float* pg = probs + (chain ? g : 0) * score_stride;
+    uint16_t* slots = reinterpret_cast<uint16_t*>(stage);  // [2][kVTile][DIM]
     float acc = 0.0f;
-    // Staging: load u of this thread covers token (tid + 256u) / kPieces of the
-    // tile, piece (tid + 256u) % kPieces.
-    int entry[kTileLoads];
-    uint4 vr[kTileLoads];
-    auto tile_token = [&](int t0, int u) { return t0 + (int(threadIdx.x) + kThreads * u) / kPieces; };
-    auto load_entries = [&](int t0) {
+    auto put = [&](const uint4 (&r)[kVLoads], const bool (&ok)[kVLoads], int slot) {
 #pragma unroll
-        for (int u = 0; u < kTileLoads; ++u) {
-            const int t = tile_token(t0, u);
-            entry[u] = t < ctx ? table[t / bs] : -1;
-        }
-    };
-    auto load_tile = [&](int t0) {
-#pragma unroll
-        for (int u = 0; u < kTileLoads; ++u) {
-            const int t = tile_token(t0, u);
-            const int piece = (int(threadIdx.x) + kThreads * u) % kPieces;
-            const int64_t ph = t < ctx ? phys_token(entry[u], t, bs, blocks) : -1;
-            vr[u] = ph >= 0 ? nvr::load_stream(vc + (ph * kvh + kvhead) * DIM + 8 * piece)
-                            : make_uint4(kNegZeroPair, kNegZeroPair, kNegZeroPair, kNegZeroPair);
-        }
-    };
-    load_entries(0);
-    load_tile(0);
-    load_entries(kVTile);
-    for (int t0 = 0; t0 < ctx; t0 += kVTile) {
-        __syncthreads();  // the previous tile is consumed
-#pragma unroll
-        for (int u = 0; u < kTileLoads; ++u)
-            *reinterpret_cast<uint4*>(vtile + 8 * (int(threadIdx.x) + kThreads * u)) = vr[u];
+        for (int u = 0; u < kVLoads; ++u)
+            *reinterpret_cast<uint4*>(slots + slot * kVTile * DIM + 8 * (int(threadIdx.x) + kThreads * u)) =
+                ok[u] ? r[u] : make_uint4(kNegZeroPair, kNegZeroPair, kNegZeroPair, kNegZeroPair);
         __syncthreads();
-        if (t0 + kVTile < ctx) {
-            load_tile(t0 + kVTile);
-            load_entries(t0 + 2 * kVTile);
-        }
+    };
+    auto consume = [&](int slot, int t0) {
         const int n = min(kVTile, ctx - t0);
-        if (chain) {
-            int j = 0;
-            for (; j + 8 <= n; j += 8) {
-                const float4 p0 = *reinterpret_cast<const float4*>(pg + t0 + j);
-                const float4 p1 = *reinterpret_cast<const float4*>(pg + t0 + j + 4);
-                float v[8];
+        if (!chain || n <= 0) return;
+        const uint16_t* vt = slots + slot * kVTile * DIM + d;
+        int j = 0;
+        for (; j + 8 <= n; j += 8) {
+            const float4 p0 = *reinterpret_cast<const float4*>(pg + t0 + j);
+            const float4 p1 = *reinterpret_cast<const float4*>(pg + t0 + j + 4);
+            float v[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) v[i] = nvr::bf16_to_f32(vtile[(j + i) * DIM + d]);
-                acc = __builtin_fmaf(p0.x, v[0], acc);
-                acc = __builtin_fmaf(p0.y, v[1], acc);
-                acc = __builtin_fmaf(p0.z, v[2], acc);
-                acc = __builtin_fmaf(p0.w, v[3], acc);
-                acc = __builtin_fmaf(p1.x, v[4], acc);
-                acc = __builtin_fmaf(p1.y, v[5], acc);
-                acc = __builtin_fmaf(p1.z, v[6], acc);
-                acc = __builtin_fmaf(p1.w, v[7], acc);
-            }
-            for (; j < n; ++j) acc = __builtin_fmaf(pg[t0 + j], nvr::bf16_to_f32(vtile[j * DIM + d]), acc);
+            for (int k = 0; k < 8; ++k) v[k] = nvr::bf16_to_f32(vt[(j + k) * DIM]);
+            acc = __builtin_fmaf(p0.x, v[0], acc);
+            acc = __builtin_fmaf(p0.y, v[1], acc);
+            acc = __builtin_fmaf(p0.z, v[2], acc);
+            acc = __builtin_fmaf(p0.w, v[3], acc);
+            acc = __builtin_fmaf(p1.x, v[4], acc);
+            acc = __builtin_fmaf(p1.y, v[5], acc);
+            acc = __builtin_fmaf(p1.z, v[6], acc);
+            acc = __builtin_fmaf(p1.w, v[7], acc);
         }
+        for (; j < n; ++j) acc = __builtin_fmaf(pg[t0 + j], nvr::bf16_to_f32(vt[j * DIM]), acc);
+    };
+    // Three register tiles in fixed roles keep two tiles in flight while one
+    // is consumed. The loads past the context stay unconditional (they hit
+    // token 0 of block 0 in L2; a branch would drain the load queue).
+    for (int i = 0, t0 = 0; t0 < ctx; i += 3, t0 += 3 * kVTile) {
+        put(rW, okW, i & 1);
+        load_vtile(rW, okW, t0 + 3 * kVTile);
+        consume(i & 1, t0);
+        if (t0 + kVTile >= ctx) break;  // uniform
+        put(rX, okX, (i + 1) & 1);
+        load_vtile(rX, okX, t0 + 4 * kVTile);
+        consume((i + 1) & 1, t0 + kVTile);
+        if (t0 + 2 * kVTile >= ctx) break;  // uniform
+        put(rY, okY, (i + 2) & 1);
+        load_vtile(rY, okY, t0 + 5 * kVTile);
+        consume((i + 2) & 1, t0 + 2 * kVTile);
     }
     if (chain) {
         float dg = den[0];
 #pragma unroll
-        for (int i = 1; i < HPB; ++i) dg = g == i ? den[i] : dg;
+        for (int k = 1; k < HPB; ++k) dg = g == k ? den[k] : dg;
         orow[g * DIM + d] = nvr::f32_to_bf16(dg > 0.0f ? acc / dg : 0.0f);
     }
 }
@@ -340,9 +420,17 @@ void launch_ordered(nv_context* c, const uint16_t* q, const uint16_t* k, const u
                     const int* s, const int* t, uint16_t* o, int rows, int qh, int kvh, int bs, int blocks,
                     int stride, int batch, int max_context) {
     const int score_stride = (max_context + 3) & ~3;
-    const size_t lds = sizeof(float) * HPB * score_stride + sizeof(uint16_t) * kVTile * DIM;
-    hipLaunchKernelGGL((attention_ordered<DIM, HPB>), dim3(unsigned(rows), unsigned(qh / HPB)), dim3(kThreads), lds,
-                       c->stream, q, k, v, p, s, t, o, qh, kvh, bs, blocks, stride, batch, max_context, score_stride);
+    const int table_entries = (max_context - 1) / bs + 1;
+    const size_t lds = sizeof(float) * HPB * score_stride + OrderedLayout<DIM, HPB>::kStageBytes +
+                       sizeof(int) * table_entries;
+    const dim3 grid(unsigned(rows), unsigned(qh / HPB));
+    if ((bs & (bs - 1)) == 0)
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, true>), grid, dim3(kThreads), lds, c->stream, q, k, v, p, s, t,
+                           o, qh, kvh, bs, __builtin_ctz(unsigned(bs)), blocks, stride, batch, max_context,
+                           score_stride);
+    else
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, false>), grid, dim3(kThreads), lds, c->stream, q, k, v, p, s,
+                           t, o, qh, kvh, bs, 0, blocks, stride, batch, max_context, score_stride);
 }
 
 template <int DIM>
@@ -375,7 +463,9 @@ extern "C" int nv_attention(nv_context* c, const void* q, const void* kc, const 
     auto s32 = static_cast<const int*>(seqs);
     auto t32 = static_cast<const int*>(tables);
     auto o16 = static_cast<uint16_t*>(out);
-    const bool vec = nvr::aligned(q, 16) && nvr::aligned(kc, 16) && nvr::aligned(vc, 16);
+    // The ordered kernels index cache rows in int32.
+    const bool vec = nvr::aligned(q, 16) && nvr::aligned(kc, 16) && nvr::aligned(vc, 16) &&
+                     int64_t(blocks) * bs <= 0x7fffffff;
     if (vec && dim == 128)
         launch_dim<128>(c, q16, k16, v16, p32, s32, t32, o16, rows, qh, kvh, bs, blocks, stride, batch, max_context);
     else if (vec && dim == 64)
