@@ -328,22 +328,21 @@ def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain, only=()):
 
     # Paged attention, decode: 64 sequences at context 4096 (one query row each).
     if want("attention_decode_64x4096"):
-        B, ctx = 64, MAX_POS
-        stride = ctx // BS
-        blocks = B * stride
-        kc = fill.normal(blocks * BS * KVH * D * 2)
-        vc = fill.normal(blocks * BS * KVH * D * 2)
-        rng = np.random.default_rng(11)
-        tables = fill.ints(rng.permutation(blocks).astype(np.int32))
-        pos = fill.ints(np.full(B, ctx - 1, np.int32))
-        seqs = fill.ints(np.arange(B, dtype=np.int32))
-        qs = [fill.normal(B * QH * D * 2) for _ in range(4)]
-        outs = [gpu.alloc(B * QH * D * 2) for _ in range(4)]
+        ab, actx = 64, MAX_POS
+        astride = actx // BS
+        ablocks = ab * astride
+        akc = fill.normal(ablocks * BS * KVH * D * 2)
+        avc = fill.normal(ablocks * BS * KVH * D * 2)
+        atab = fill.ints(np.random.default_rng(11).permutation(ablocks).astype(np.int32))
+        apos = fill.ints(np.full(ab, actx - 1, np.int32))
+        aseq = fill.ints(np.arange(ab, dtype=np.int32))
+        aq = [fill.normal(ab * QH * D * 2) for _ in range(4)]
+        aout = [gpu.alloc(ab * QH * D * 2) for _ in range(4)]
         cases.append(("attention_decode_64x4096", "paged GQA attention, 64 decode rows x 4096 context, 16/8 heads, "
                       "dim 128, 256-token blocks (K+V 1.07 GB per launch)",
-                      [lambda i=i: gpu.paged_attention(qs[i], kc, vc, pos, seqs, tables, outs[i], B, QH, KVH, D, BS,
-                                                       blocks, stride, B, ctx) for i in range(4)],
-                      bytes_attention(B, ctx, stride), B))
+                      [lambda i=i: gpu.paged_attention(aq[i], akc, avc, apos, aseq, atab, aout[i], ab, QH, KVH, D, BS,
+                                                       ablocks, astride, ab, actx) for i in range(4)],
+                      bytes_attention(ab, actx, astride), ab))
 
     # Sampling 256 x 151936: rows 0-127 greedy, 128-255 Gumbel at T=0.6.
     if not want("sampling_256x151936", "sampling_greedy", "sampling_gumbel"):
