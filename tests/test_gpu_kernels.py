@@ -176,6 +176,16 @@ def test_silu_8192x3072(gpu):
     assert np.mean(d == 0) > 0.999
 
 
+@pytest.mark.parametrize("rows,inter", [(7, 296), (3, 2056), (1, 8), (513, 24)])
+def test_silu_blocks_straddling_rows(gpu, rows, inter):
+    """The flat grid puts chunks of consecutive rows in one block; chunk counts
+    per row of 37, 257, 1 and 3 cross every block boundary case."""
+    gu = ora.normal_bf16((rows, 2, inter), 92 + rows, 0.0, 2.0)
+    out = gpu.alloc(rows * inter * 2)
+    gpu.silu_mul(up(gpu, gu), out, rows, inter)
+    assert bf16_ulp_diff(down(out, np.uint16, (rows, inter)), ora.silu(gu, rows, inter)).max() <= 1
+
+
 def test_silu_edges_and_generic(gpu):
     g = np.array([-1e4, -100.0, -88.5, -87.0, -20.0, -0.0, 0.0, 1e-30, 3.0, 88.0, 1e4, np.inf, -np.inf, np.nan, 1.0,
                   -1.0], np.float32)
