@@ -88,24 +88,32 @@ __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict_
     constexpr int D = 128, HALF = 64, GROUPS = kWave / kHeadLanes, DEPTH = 4, SPLIT = 2;
     const int lane = threadIdx.x & (kWave - 1);
     const int grp = lane / kHeadLanes, m = lane & (kHeadLanes - 1);
-    const int64_t wave = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
-    const int64_t row = wave / SPLIT;
-    const int hw = int(wave - row * SPLIT);
+    // The wave's row is uniform: make it a scalar so position and slot come
+    // from scalar loads (their own counter), not from the vector queue behind
+    // the head loads.
+    const int wave = __builtin_amdgcn_readfirstlane(int(blockIdx.x) * int(blockDim.x / kWave) +
+                                                    int(threadIdx.x / kWave));
+    const int row = wave / SPLIT;
+    const int hw = wave - row * SPLIT;
     if (row >= rows) return;  // uniform per wave
     const int heads = qh + 2 * kvh;
-    const uint16_t* src = qkv + row * heads * D + 8 * m;
+    const uint16_t* src = qkv + int64_t(row) * heads * D + 8 * m;
     // Head of slot j in pass `pass`: quad hw + SPLIT * (j + DEPTH * pass).
+    // Loads are unconditional (a head index past the row is clamped and its
+    // data unused): a branch around a load makes the compiler wait for the
+    // whole load queue before the first head is processed.
     auto head_of = [&](int pass, int j) { return GROUPS * (hw + SPLIT * (j + DEPTH * pass)) + grp; };
     uint4 xw[DEPTH];
 #pragma unroll
-    for (int j = 0; j < DEPTH; ++j) {
-        const int h = head_of(0, j);
-        if (h < heads) xw[j] = nvr::load_stream(src + int64_t(h) * D);
-    }
+    for (int j = 0; j < DEPTH; ++j) xw[j] = nvr::load_stream(src + int64_t(min(head_of(0, j), heads - 1)) * D);
     const int pos = positions[row];
     const int slot = slots[row];
     const bool valid_slot = slot >= 0 && int64_t(slot) < int64_t(bs) * blocks;
 
+    // Norm weights and the position's cos/sin are requested before anything
+    // waits on a load, so all of a wave's loads are in flight together.
+    const uint4 qwv = *reinterpret_cast<const uint4*>(qw + 8 * m);
+    const uint4 kwv = *reinterpret_cast<const uint4*>(kw + 8 * m);
     const int pair0 = 8 * (m & 7);
     float cs[8], sn[8];
     if constexpr (CACHED) {
@@ -130,17 +138,15 @@ __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict_
         for (int i = 0; i < 8; ++i) sn[i] = -sn[i];
     }
     float qwf[8], kwf[8];
-    nvr::unpack8(*reinterpret_cast<const uint4*>(qw + 8 * m), qwf);
-    nvr::unpack8(*reinterpret_cast<const uint4*>(kw + 8 * m), kwf);
+    nvr::unpack8(qwv, qwf);
+    nvr::unpack8(kwv, kwf);
 
     // Uniform trip count: a pass runs while its first quad exists.
     for (int pass = 0; GROUPS * (hw + SPLIT * DEPTH * pass) < heads; ++pass) {
         if (pass > 0) {  // rows with more than 32 heads
 #pragma unroll
-            for (int j = 0; j < DEPTH; ++j) {
-                const int h = head_of(pass, j);
-                if (h < heads) xw[j] = nvr::load_stream(src + int64_t(h) * D);
-            }
+            for (int j = 0; j < DEPTH; ++j)
+                xw[j] = nvr::load_stream(src + int64_t(min(head_of(pass, j), heads - 1)) * D);
         }
 #pragma unroll
         for (int j = 0; j < DEPTH; ++j) {
@@ -149,7 +155,8 @@ __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict_
             if (h >= qh + kvh) {  // V head: bit copy into the cache
                 if (valid_slot) nvr::store_stream(vc + (int64_t(slot) * kvh + (h - qh - kvh)) * D + 8 * m, xw[j]);
             } else if (h < qh) {
-                nvr::store_stream(qout + (row * qh + h) * D + 8 * m, norm_rotate_d128(xw[j], qwf, cs, sn, eps));
+                nvr::store_stream(qout + (int64_t(row) * qh + h) * D + 8 * m,
+                                  norm_rotate_d128(xw[j], qwf, cs, sn, eps));
             } else {
                 const uint4 rot = norm_rotate_d128(xw[j], kwf, cs, sn, eps);
                 if (valid_slot) nvr::store_stream(kc + (int64_t(slot) * kvh + (h - qh)) * D + 8 * m, rot);
