@@ -278,7 +278,7 @@ def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain, only=()):
                       [lambda i=i, T=T: gpu.silu_mul(gus[i], acts[i], T, I) for i in range(s)], bytes_silu(T, I), T))
 
     # q/k norm + RoPE + KV write at 2048 and 8192 tokens, uniform random positions.
-    for T in (2048, 8192):
+    for T in (2048, 4096, 8192):
         if not want(f"qkv_rope_{T}"):
             continue
         rng = np.random.default_rng(T)

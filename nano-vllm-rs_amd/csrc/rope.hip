@@ -30,6 +30,8 @@ namespace {
 using nvr::kWave;
 
 constexpr int kHeadLanes = 16;
+// Row count from which the d128 kernel uses four waves per row instead of two.
+constexpr int kRopeSplit4Rows = 4096;
 
 // q/k head: RMSNorm in the reference's order, bf16 rounding, NeoX rotation.
 // Returns the rotated chunk of this lane (elements 8m..8m+7), packed. The
@@ -72,20 +74,21 @@ __device__ __forceinline__ uint4 norm_rotate_d128(const uint4& xw, const float* 
     return nvr::pack8(o);
 }
 
-// Two waves per token row. The row's heads form quads 4Q..4Q+3; wave half
-// hw takes quads hw, hw+2, hw+4, ... (for 16 q + 8 k + 8 v heads each half
-// gets 8 q, 4 k and 4 v heads), and group g (16 lanes) of the wave takes head
-// 4Q + g of each of its quads. Lane m of a group holds elements 8m..8m+7 of a
-// head. All head loads of a lane are issued first; position, slot, cos/sin
-// and the norm weights are read once per wave.
-template <bool CACHED>
+// SPLIT waves per token row. The row's heads form quads 4Q..4Q+3; wave part
+// hw takes quads hw, hw+SPLIT, hw+2*SPLIT, ... and group g (16 lanes) of the
+// wave takes head 4Q + g of each of its quads. Lane m of a group holds
+// elements 8m..8m+7 of a head. All head loads of a lane are issued first;
+// position, slot, cos/sin and the norm weights are read once per wave. Four
+// waves per row (2 quads each, 67 VGPRs, 7 waves per SIMD) measured fastest
+// at 8192 rows, two waves per row (4 quads each) at 2048 rows.
+template <bool CACHED, int SPLIT>
 __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qw,
                                                      const uint16_t* __restrict__ kw, const int* __restrict__ positions,
                                                      const int* __restrict__ slots, uint16_t* __restrict__ qout,
                                                      uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int rows,
                                                      int qh, int kvh, int bs, int blocks, float eps, float theta,
                                                      const float* __restrict__ table, int max_positions) {
-    constexpr int D = 128, HALF = 64, GROUPS = kWave / kHeadLanes, DEPTH = 4, SPLIT = 2;
+    constexpr int D = 128, HALF = 64, GROUPS = kWave / kHeadLanes, DEPTH = 8 / SPLIT;
     const int lane = threadIdx.x & (kWave - 1);
     const int grp = lane / kHeadLanes, m = lane & (kHeadLanes - 1);
     // The wave's row is uniform: make it a scalar so position and slot come
@@ -277,12 +280,18 @@ int launch_qkv_rope(nv_context* c, const void* qkv, const void* qw, const void* 
     auto k16 = static_cast<uint16_t*>(kc);
     auto v16 = static_cast<uint16_t*>(vc);
     auto tab = static_cast<const float*>(table);
-    const bool vec = dim == 128 && nvr::aligned(qkv, 16) && nvr::aligned(qw, 16) && nvr::aligned(kw, 16) &&
+    const bool vec = dim == 128 && rows <= (1 << 28) && nvr::aligned(qkv, 16) && nvr::aligned(qw, 16) &&
+                     nvr::aligned(kw, 16) &&
                      nvr::aligned(qout, 16) && nvr::aligned(kc, 16) && nvr::aligned(vc, 16) &&
                      (!CACHED || nvr::aligned(table, 16));
-    if (vec) {
+    if (vec && rows >= kRopeSplit4Rows) {
+        const int64_t nblocks = int64_t(rows);  // four waves per row
+        if (nblocks > 0x7fffffff) return nvr::fail(-2, "qkv_rope: too many rows for one launch");
+        hipLaunchKernelGGL((qkv_rope_d128<CACHED, 4>), dim3(unsigned(nblocks)), dim3(256), 0, c->stream, q16, qw16,
+                           kw16, pos, sl, qo, k16, v16, rows, qh, kvh, bs, blocks, eps, theta, tab, max_positions);
+    } else if (vec) {
         const int64_t nblocks = (int64_t(rows) * 2 + 3) / 4;  // two waves per row
-        hipLaunchKernelGGL((qkv_rope_d128<CACHED>), dim3(unsigned(nblocks)), dim3(256), 0, c->stream, q16, qw16,
+        hipLaunchKernelGGL((qkv_rope_d128<CACHED, 2>), dim3(unsigned(nblocks)), dim3(256), 0, c->stream, q16, qw16,
                            kw16, pos, sl, qo, k16, v16, rows, qh, kvh, bs, blocks, eps, theta, tab, max_positions);
     } else {
         const int64_t nblocks = (pairs + 3) / 4;

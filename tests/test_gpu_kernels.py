@@ -141,6 +141,23 @@ def test_qkv_rope_cached_8192_tokens(gpu):
     _rope_case(gpu, rows, 16, 8, 128, bs, blocks, 50, pos, unique_slots(rows, bs, blocks, 14))
 
 
+@pytest.mark.parametrize("qh,kvh,cached", [(16, 8, False), (32, 8, True), (8, 8, True), (12, 2, True)])
+def test_qkv_rope_four_waves_per_row(gpu, qh, kvh, cached):
+    """From 4096 rows the d128 kernel spreads a row over four waves: head
+    counts that are not 32 (extra passes, partial quads), the uncached angle
+    path, and out-of-range positions and slots."""
+    rows, bs = 4096, 256
+    blocks = rows // bs
+    rng = np.random.default_rng(qh * 10 + kvh)
+    pos = rng.integers(0, 4096, rows).astype(np.int32)
+    pos[::97] = -5
+    pos[1::89] = 4200
+    slots = unique_slots(rows, bs, blocks, qh + kvh)
+    slots[::53] = -1
+    slots[2::71] = bs * blocks + 3
+    _rope_case(gpu, rows, qh, kvh, 128, bs, blocks, 300 + qh, pos, slots, cached=cached)
+
+
 def test_qkv_rope_guards(gpu):
     """Positions outside the table rotate by 0; slots outside the cache are skipped."""
     rows, bs, blocks = 12, 4, 4
