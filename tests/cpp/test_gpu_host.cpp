@@ -1,0 +1,348 @@
+// The reference's own GPU tests (src/gpu.rs:1148-1472 of nano-vllm-rs),
+// restated over the C++ host API (nano-vllm-rs_amd/host/gpu.hpp), plus
+// CPU-only checks of its argument validation.
+//
+// Usage: test_gpu_host cpu|gpu   -> runs that suite, exit status 0 when all pass.
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "gpu.hpp"
+
+namespace {
+
+struct Case {
+    const char* name;
+    const char* kind;
+    void (*fn)();
+};
+std::vector<Case>& registry() {
+    static std::vector<Case> cases;
+    return cases;
+}
+struct Registrar {
+    Registrar(const char* name, const char* kind, void (*fn)()) { registry().push_back({name, kind, fn}); }
+};
+struct Failure {
+    std::string what;
+};
+
+#define TEST(name, kind)                                   \
+    static void name();                                    \
+    static Registrar registrar_##name(#name, kind, name); \
+    static void name()
+#define CHECK(cond)                                                                                     \
+    do {                                                                                                \
+        if (!(cond)) throw Failure{std::string(__FILE__ ":") + std::to_string(__LINE__) + ": " #cond}; \
+    } while (0)
+#define CHECK_THROWS(expr)                                                                                  \
+    do {                                                                                                    \
+        bool thrown_ = false;                                                                               \
+        try {                                                                                               \
+            expr;                                                                                           \
+        } catch (const nvr::Error&) {                                                                       \
+            thrown_ = true;                                                                                 \
+        }                                                                                                   \
+        if (!thrown_) throw Failure{std::string(__FILE__ ":") + std::to_string(__LINE__) + ": no throw: " #expr}; \
+    } while (0)
+
+// bf16 bit patterns, round to nearest even, NaN kept quiet.
+std::vector<uint8_t> bf16(const std::vector<float>& values) {
+    std::vector<uint8_t> out;
+    out.reserve(values.size() * 2);
+    for (float x : values) {
+        uint32_t b;
+        std::memcpy(&b, &x, 4);
+        const uint16_t h = (b & 0x7fffffffu) > 0x7f800000u ? uint16_t((b >> 16) | 0x40)
+                                                          : uint16_t((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+        out.push_back(uint8_t(h & 0xff));
+        out.push_back(uint8_t(h >> 8));
+    }
+    return out;
+}
+
+std::vector<float> values(const nvr::Buffer& buffer, std::size_t count) {
+    const std::vector<uint16_t> bits = buffer.download_u16(count);
+    std::vector<float> out(count);
+    for (std::size_t i = 0; i < count; ++i) {
+        const uint32_t b = uint32_t(bits[i]) << 16;
+        std::memcpy(&out[i], &b, 4);
+    }
+    return out;
+}
+
+// -------------------------------------------------------------- CPU suite --
+TEST(dimension_extent_and_positive_checks, "cpu") {
+    CHECK(nvr::dimension(1) == 1);
+    CHECK(nvr::dimension(0x7fffffff) == 0x7fffffff);
+    CHECK_THROWS(nvr::dimension(0));
+    CHECK_THROWS(nvr::dimension(std::size_t(0x80000000u)));
+    CHECK(nvr::extent({3, 5}, 2) == 30);
+    CHECK_THROWS(nvr::extent({3, 0}, 2));
+    CHECK_THROWS(nvr::extent({0x7fffffff, 0x7fffffff, 0x7fffffff}, 8));  // byte count overflow
+    nvr::positive(1e-6f, "eps");
+    CHECK_THROWS(nvr::positive(0.0f, "eps"));
+    CHECK_THROWS(nvr::positive(-1.0f, "eps"));
+    CHECK_THROWS(nvr::positive(INFINITY, "eps"));
+    CHECK_THROWS(nvr::positive(NAN, "eps"));
+    try {
+        nvr::positive(0.0f, "RMS epsilon");
+    } catch (const nvr::Error& e) {
+        CHECK(std::string(e.what()) == "RMS epsilon must be positive and finite");
+    }
+}
+
+TEST(head_shape_checks, "cpu") {  // src/gpu.rs:643-660
+    nvr::heads(16, 8, 128);
+    nvr::heads(1, 1, 256);
+    CHECK_THROWS(nvr::heads(16, 6, 128));     // not a multiple
+    CHECK_THROWS(nvr::heads(16, 8, 127));     // odd
+    CHECK_THROWS(nvr::heads(16, 8, 258));     // above 256
+    CHECK_THROWS(nvr::heads(65535, 1, 128));  // qheads + kvheads > 65535
+    CHECK_THROWS(nvr::heads(0, 1, 128));
+}
+
+TEST(device_index_and_seed, "cpu") {
+    CHECK_THROWS(nvr::Gpu(-1));
+    // src/runtime.rs:780-790: mix(mix(base) ^ mix(request) ^ mix(generated)),
+    // mix = SplitMix64. With all zeros it is mix(mix(0)), mix(0) being the
+    // published 0xe220a8397b1dcdaf; request and generated commute.
+    CHECK(nvr::sampling_seed(0, 0, 0) == 0xa706dd2f4d197e6full);
+    CHECK(nvr::sampling_seed(0, 1, 2) == nvr::sampling_seed(0, 2, 1));
+}
+
+// -------------------------------------------------------------- GPU suite --
+TEST(gpu_views_keep_allocations_and_reject_overlap, "gpu") {  // src/gpu.rs:1169-1192
+    nvr::Gpu gpu(0);
+    nvr::Buffer packed = gpu.alloc(32);
+    packed.upload_i32({1, 3, 0, 0, 5, 6, 7, 8});
+    nvr::Buffer tokens = packed.slice(0, 8);
+    nvr::Buffer adjacent = packed.slice(8, 8);
+    nvr::Gpu::distinct(tokens, {&adjacent});
+    const nvr::Buffer straddling = packed.slice(4, 8);
+    CHECK_THROWS(nvr::Gpu::distinct(tokens, {&straddling}));
+    CHECK_THROWS(tokens.slice(4, 8));
+    CHECK_THROWS(packed.slice(SIZE_MAX, 1));
+    CHECK_THROWS(gpu.tensor(packed.slice(1, 8), {1}, 4));
+    nvr::Buffer weights = gpu.alloc(8);
+    weights.upload_bytes(bf16({1, 2, 3, 4}));
+    nvr::Buffer out = gpu.alloc(4);
+    nvr::Graph graph = gpu.capture([&] { gpu.embedding(tokens, weights, out, 2, 1, 4); });
+    {  // the graph keeps the views' allocation alive
+        nvr::Buffer gone = std::move(tokens), also = std::move(adjacent), last = std::move(packed);
+    }
+    graph.replay();
+    CHECK((values(out, 2) == std::vector<float>{2, 4}));
+}
+
+TEST(gpu_parallel_sampler_matches_serial_for_tail_ties_and_temperature, "gpu") {  // src/gpu.rs:1194-1244
+    nvr::Gpu gpu(0);
+    const std::size_t batch = 3, vocab = 151936, parts = (vocab + 2047) / 2048;
+    std::vector<float> scores(batch * vocab);
+    for (std::size_t i = 0; i < scores.size(); ++i) scores[i] = (float(i * 31 % 101) - 50.0f) * 0.125f;
+    scores[2047] = scores[2048] = scores[4096] = 100.0f;
+    nvr::Buffer logits = gpu.alloc(batch * vocab * 2);
+    logits.upload_bytes(bf16(scores));
+    nvr::Buffer temps = gpu.alloc(batch * 4), seeds = gpu.alloc(batch * 8);
+    temps.upload_f32({0.0f, 0.6f, 1.0f});
+    seeds.upload_u64({42, 43, 44});
+    nvr::Buffer serial = gpu.alloc(batch * 4), parallel = gpu.alloc(batch * 4);
+    nvr::Buffer ps = gpu.alloc(batch * parts * 4), pi = gpu.alloc(batch * parts * 4);
+    gpu.sample(logits, temps, seeds, serial, batch, vocab);
+    gpu.sample_parallel(logits, temps, seeds, parallel, ps, pi, batch, vocab);
+    const std::vector<int32_t> expected = serial.download_i32(batch);
+    CHECK(expected[0] == 2047);
+    CHECK(parallel.download_i32(batch) == expected);
+    nvr::Graph graph = gpu.capture([&] { gpu.sample_parallel(logits, temps, seeds, parallel, ps, pi, batch, vocab); });
+    graph.replay();
+    CHECK(parallel.download_i32(batch) == expected);
+}
+
+TEST(gpu_cached_rope_matches_direct_at_context_boundary, "gpu") {  // src/gpu.rs:1246-1289
+    nvr::Gpu gpu(0);
+    const std::size_t rows = 4, qh = 4, kvh = 2, dim = 128;
+    std::vector<float> input(rows * (qh + 2 * kvh) * dim);
+    for (std::size_t i = 0; i < input.size(); ++i) input[i] = (float(i * 17 % 37) - 18.0f) / 8.0f;
+    nvr::Buffer packed = gpu.alloc(input.size() * 2);
+    packed.upload_bytes(bf16(input));
+    nvr::Buffer norm = gpu.alloc(dim * 2);
+    norm.upload_bytes(bf16(std::vector<float>(dim, 1.0f)));
+    nvr::Buffer positions = gpu.alloc(rows * 4), slots = gpu.alloc(rows * 4);
+    positions.upload_i32({0, 1, 350, 4095});
+    slots.upload_i32({0, 1, 2, 3});
+    nvr::Buffer dq = gpu.alloc(rows * qh * dim * 2), dk = gpu.alloc(4 * kvh * dim * 2), dv = gpu.alloc(4 * kvh * dim * 2);
+    nvr::Buffer cq = gpu.alloc(rows * qh * dim * 2), ck = gpu.alloc(4 * kvh * dim * 2), cv = gpu.alloc(4 * kvh * dim * 2);
+    nvr::Buffer cache = gpu.alloc(4096 * dim * 4);
+    gpu.rope_cache(cache, 4096, dim, 1e6f);
+    gpu.qkv_rope(packed, norm, norm, positions, slots, dq, dk, dv, rows, qh, kvh, dim, 4, 1, 1e-6f, 1e6f);
+    gpu.qkv_rope_cached(packed, norm, norm, positions, slots, cq, ck, cv, rows, qh, kvh, dim, 4, 1, 1e-6f, cache,
+                        4096);
+    CHECK(dq.download_bytes(dq.len()) == cq.download_bytes(cq.len()));
+    CHECK(dk.download_bytes(dk.len()) == ck.download_bytes(ck.len()));
+    CHECK(dv.download_bytes(dv.len()) == cv.download_bytes(cv.len()));
+}
+
+TEST(gpu_gemm_rms_sampling_graph, "gpu") {  // src/gpu.rs:1290-1330
+    nvr::Gpu gpu(0);
+    nvr::Buffer x = gpu.alloc(12), w = gpu.alloc(12), y = gpu.alloc(8);
+    x.upload_bytes(bf16({1, 2, 3, 4, 5, 6}));
+    w.upload_bytes(bf16({1, 0, 1, 0, 1, 0}));
+    gpu.gemm(x, w, y, 2, 2, 3);
+    CHECK((values(y, 4) == std::vector<float>{4, 2, 10, 5}));
+    CHECK_THROWS(gpu.gemm(x, w, y, 3, 2, 3));
+    CHECK_THROWS(gpu.gemm(x, w, x, 2, 2, 3));
+    nvr::Buffer normw = gpu.alloc(4), normalized = gpu.alloc(8);
+    normw.upload_bytes(bf16({1, 1}));
+    gpu.rms_norm(y, normw, normalized, 2, 2, 1e-6f);
+    CHECK(std::fabs(values(normalized, 4)[0] - 1.264911f) < 0.008f);
+    nvr::Buffer temps = gpu.alloc(8), seeds = gpu.alloc(16), output = gpu.alloc(8);
+    temps.upload_f32({0, 0});
+    seeds.upload_u64({42, 43});
+    gpu.sample(y, temps, seeds, output, 2, 2);
+    CHECK((output.download_i32(2) == std::vector<int32_t>{0, 0}));
+    gpu.sync();
+    nvr::Graph graph = gpu.capture([&] { gpu.gemm(x, w, y, 2, 2, 3); });
+    x.upload_bytes(bf16({2, 4, 6, 8, 10, 12}));
+    graph.replay();
+    CHECK((values(y, 4) == std::vector<float>{8, 4, 20, 10}));
+    {  // captured allocations remain valid when their handles drop
+        nvr::Buffer gone = std::move(x), also = std::move(w);
+    }
+    graph.replay();
+    gpu.sync();
+    CHECK_THROWS(gpu.capture([&] { gpu.alloc(4); }));
+    gpu.sync();  // the failed capture left the context usable
+}
+
+TEST(gpu_causal_paged_attention_and_rope, "gpu") {  // src/gpu.rs:1330-1380
+    nvr::Gpu gpu(0);
+    const std::size_t rows = 3, dim = 32, qh = 2, kvh = 1;
+    nvr::Buffer q = gpu.alloc(rows * qh * dim * 2);
+    nvr::Buffer k = gpu.alloc(2 * 2 * kvh * dim * 2), v = gpu.alloc(2 * 2 * kvh * dim * 2);
+    std::vector<float> cache(4 * dim, 0.0f);  // reversed physical blocks: logical token values 1, 2, 3
+    for (std::size_t d = 0; d < dim; ++d) {
+        cache[2 * dim + d] = 1;
+        cache[3 * dim + d] = 2;
+        cache[d] = 3;
+    }
+    v.upload_bytes(bf16(cache));
+    nvr::Buffer positions = gpu.alloc(rows * 4), seqs = gpu.alloc(rows * 4), tables = gpu.alloc(8);
+    positions.upload_i32({0, 1, 2});
+    seqs.upload_i32({0, 0, 0});
+    tables.upload_i32({1, 0});
+    nvr::Buffer out = gpu.alloc(rows * qh * dim * 2);
+    gpu.paged_attention(q, k, v, positions, seqs, tables, out, rows, qh, kvh, dim, 2, 2, 2, 1, 4);
+    const std::vector<float> actual = values(out, rows * qh * dim);
+    for (std::size_t r = 0; r < rows; ++r)
+        for (std::size_t d = 0; d < qh * dim; ++d) CHECK(actual[r * qh * dim + d] == 1.0f + float(r) * 0.5f);
+    nvr::Buffer packed = gpu.alloc(rows * (qh + 2 * kvh) * dim * 2);
+    packed.upload_bytes(bf16(std::vector<float>(rows * (qh + 2 * kvh) * dim, 1.0f)));
+    nvr::Buffer weight = gpu.alloc(dim * 2);
+    weight.upload_bytes(bf16(std::vector<float>(dim, 1.0f)));
+    nvr::Buffer slots = gpu.alloc(rows * 4);
+    slots.upload_i32({2, 3, 0});
+    gpu.qkv_rope(packed, weight, weight, positions, slots, q, k, v, rows, qh, kvh, dim, 2, 2, 1e-6f, 1e6f);
+    const std::vector<float> qv = values(q, rows * qh * dim);
+    for (std::size_t i = 0; i < qh * dim; ++i) CHECK(std::fabs(qv[i] - 1.0f) < 0.01f);
+    CHECK(std::fabs(qv[qh * dim] - (std::cos(1.0f) - std::sin(1.0f))) < 0.008f);
+    CHECK(values(v, 4 * dim)[0] == 1.0f);
+}
+
+void ragged_gqa_case(std::size_t dim, std::size_t block_size, std::vector<int32_t> pos, std::vector<int32_t> seq,
+                     std::vector<int32_t> table) {  // src/gpu.rs:1382-1470
+    nvr::Gpu gpu(0);
+    const std::size_t rows = 4, qheads = 4, kvheads = 2, blocks = 4;
+    std::vector<float> qv(rows * qheads * dim), kv(blocks * block_size * kvheads * dim), vv(kv.size());
+    for (std::size_t i = 0; i < qv.size(); ++i) qv[i] = (float(i * 7 % 19) - 9.0f) * 0.125f;
+    for (std::size_t i = 0; i < kv.size(); ++i) kv[i] = (float(i * 11 % 23) - 11.0f) * 0.125f;
+    for (std::size_t i = 0; i < vv.size(); ++i) vv[i] = (float(i * 3 % 13) - 6.0f) * 0.125f;
+    nvr::Buffer q = gpu.alloc(qv.size() * 2), k = gpu.alloc(kv.size() * 2), v = gpu.alloc(vv.size() * 2);
+    q.upload_bytes(bf16(qv));
+    k.upload_bytes(bf16(kv));
+    v.upload_bytes(bf16(vv));
+    nvr::Buffer positions = gpu.alloc(rows * 4), sequences = gpu.alloc(rows * 4), tables = gpu.alloc(table.size() * 4);
+    positions.upload_i32(pos);
+    sequences.upload_i32(seq);
+    tables.upload_i32(table);
+    nvr::Buffer out = gpu.alloc(qv.size() * 2);
+    int32_t max_pos = 0;
+    for (int32_t p : pos) max_pos = p > max_pos ? p : max_pos;
+    gpu.paged_attention(q, k, v, positions, sequences, tables, out, rows, qheads, kvheads, dim, block_size, blocks, 2,
+                        table.size() / 2, std::size_t(max_pos) + 1);
+    const std::vector<float> actual = values(out, qv.size());
+    for (std::size_t row = 0; row < rows; ++row) {
+        const std::size_t context = std::size_t(pos[row]) + 1;
+        for (std::size_t head = 0; head < qheads; ++head) {
+            const std::size_t kvhead = head / (qheads / kvheads), qbase = (row * qheads + head) * dim;
+            auto base = [&](std::size_t t) {
+                return ((std::size_t(table[std::size_t(seq[row]) * 2 + t / block_size]) * block_size + t % block_size) *
+                            kvheads +
+                        kvhead) *
+                       dim;
+            };
+            std::vector<float> scores(context);
+            float mx = -INFINITY;
+            for (std::size_t t = 0; t < context; ++t) {
+                float s = 0;
+                for (std::size_t d = 0; d < dim; ++d) s += qv[qbase + d] * kv[base(t) + d];
+                scores[t] = s / std::sqrt(float(dim));
+                mx = std::fmax(mx, scores[t]);
+            }
+            float sum = 0;
+            for (float& s : scores) sum += (s = std::exp(s - mx));
+            for (std::size_t d = 0; d < dim; ++d) {
+                float expected = 0;
+                for (std::size_t t = 0; t < context; ++t) expected += scores[t] * vv[base(t) + d];
+                CHECK(std::fabs(actual[qbase + d] - expected / sum) < 0.004f);
+            }
+        }
+    }
+}
+
+TEST(gpu_ragged_gqa_matches_cpu, "gpu") {
+    ragged_gqa_case(32, 2, {0, 2, 1, 0}, {0, 0, 1, 2}, {3, 1, 0, 2, 2, -1});
+    ragged_gqa_case(128, 256, {0, 255, 256, 510}, {0, 0, 1, 1}, {3, 1, 0, 2});
+}
+
+TEST(gpu_capture_failure_leaves_the_context_usable, "gpu") {
+    nvr::Gpu gpu(0);
+    nvr::Buffer a = gpu.alloc(64), b = gpu.alloc(64);
+    CHECK_THROWS(gpu.capture([&] { gpu.silu_mul(a, a, 1, 16); }));  // output aliases the input
+    gpu.sync();
+    nvr::Graph graph = gpu.capture([&] { gpu.silu_mul(a, b, 1, 16); });
+    graph.replay();
+    gpu.sync();
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc < 2 || (std::strcmp(argv[1], "cpu") != 0 && std::strcmp(argv[1], "gpu") != 0)) {
+        std::fprintf(stderr, "usage: %s cpu|gpu\n", argv[0]);
+        return 2;
+    }
+    int failed = 0, ran = 0;
+    for (const Case& c : registry()) {
+        if (std::strcmp(c.kind, argv[1]) != 0) continue;
+        ++ran;
+        std::printf("%s ... ", c.name);
+        std::fflush(stdout);
+        try {
+            c.fn();
+            std::printf("ok\n");
+        } catch (const Failure& f) {
+            ++failed;
+            std::printf("FAILED: %s\n", f.what.c_str());
+        } catch (const std::exception& e) {
+            ++failed;
+            std::printf("FAILED: exception: %s\n", e.what());
+        }
+        std::fflush(stdout);
+    }
+    std::printf("%d of %d passed\n", ran - failed, ran);
+    return failed == 0 && ran > 0 ? 0 : 1;
+}
