@@ -374,6 +374,54 @@ def test_sampling_pruning_edges(gpu):
     assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab, parallel=False), want)
 
 
+def _edge_rows(batch, vocab, seed):
+    """Rows that stress exact pruning and the total order (see the comments),
+    then ordinary rows with mixed temperatures."""
+    seeds = np.array([ora.sampling_seed(seed, r, 7) for r in range(batch)], np.uint64)
+    temps = np.array([(0.0, 0.6, 1.3)[r % 3] for r in range(batch)], np.float32)
+    logits = ora.normal_bf16((batch, vocab), seed + 1, 0.0, 3.0)
+    idx = np.arange(vocab)
+    temps[:7] = (0.6, 1.7, 1e-4, 1e4, 0.6, 0.6, 0.6)
+    for r, base in ((0, 6.0), (1, -2.0)):  # every score ~ base / T: all tokens candidates
+        logits[r] = bf16_of(np.float32(base) - temps[r] * _noise(float(temps[r]), int(seeds[r]), vocab))
+    logits[4] = bf16_of(np.ones(vocab, np.float32))  # equal logits
+    for r in (5, 6):  # the largest logit against the largest noise, tied (5) or one step apart (6)
+        noise = _noise(float(temps[r]), int(seeds[r]), vocab)
+        m = int(np.argmax(f32_of(logits[r])))
+        j = int(np.argmax(np.where(idx == m, -np.inf, noise)))
+        target = np.float32(f32_of(logits[r, m]) - temps[r] * (noise[j] - noise[m]))
+        logits[r, j] = bf16_of(target + (np.float32(0.0) if r == 5 else np.float32(abs(target) * 2**-7)))
+    special = {
+        7: np.full(vocab, np.nan),
+        8: np.full(vocab, -np.inf),
+        9: np.where(idx == vocab // 3, np.inf, np.nan),
+        10: np.r_[np.full(vocab - 1, -1.0), 5.0],
+        11: np.where(idx % 2048 == 2047, 9.0, 0.0),
+        16: np.where(idx % 1000 == 999, np.inf, 1.0),  # s0 = +inf: no pruning
+        17: np.where(idx % 777 == 5, 3e38, -3e38),  # logit / T overflows
+        18: np.where(idx < vocab // 2, -np.inf, np.nan),
+    }
+    for r, row in special.items():
+        logits[r] = bf16_of(row)
+        temps[r] = 0.8
+    temps[12], temps[13], temps[14], temps[15], temps[17] = 1e-40, np.inf, np.nan, -1.0, 1e-3
+    return logits, temps, seeds
+
+
+@pytest.mark.parametrize("vocab", [3 * 4096 + 8, 40000, 90000, 131072, 163840, 163848])
+def test_sampling_large_batches(gpu, vocab):
+    """From one row per CU, rows of up to 163840 tokens are sampled by one
+    block per row holding the row in registers; parity with the serial scan
+    and the oracle on rows that stress pruning, special values and
+    temperatures, for every register-tile width (4 to 20 chunks a lane) and
+    just past the limit."""
+    batch = max(256, gpu.sm_count())
+    logits, temps, seeds = _edge_rows(batch, vocab, 180 + vocab % 97)
+    want = ora.sample(logits, temps, seeds, batch, vocab, threads=8)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab), want)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab, parallel=False), want)
+
+
 def test_sampling_reference_golden_vectors(gpu):
     import os
 

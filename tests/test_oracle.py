@@ -89,6 +89,32 @@ def test_logf_is_faithful_on_the_whole_gumbel_domain():
     assert np.float32(bound) == np.float32(-l2.min())
 
 
+def test_gumbel_noise_floors_are_lower_bounds():
+    """The row-resident sampler rejects a candidate when its hash value m is
+    below floor_k, the bound it computes for noise level D_k = -4 + k/16. That
+    is exact only if every m whose noise -ln(-ln u) reaches D_k is >= floor_k:
+    checked here for every k against the noise of all 2^23 hash values, with
+    floor_k computed by the same operations (nvr_expf = ora_expf)."""
+    src = open(os.path.join(os.path.dirname(__file__), "..", "nano-vllm-rs_amd", "csrc", "sample.hip")).read()
+    steps = int(re.search(r"kFloorSteps = (\d+);", src).group(1))
+    assert "float(k) * 0.0625f - 4.0f" in src and "(d - 0x1.0p-12f)" in src and "* 8388608.0f) - 64.0f" in src
+    k = np.arange(1 << 23, dtype=np.float32)
+    u = (k + np.float32(0.5)) * np.float32(1.0 / 8388608.0)
+    noise = -ora.logf_array(-ora.logf_array(u))
+    reach = np.maximum.accumulate(noise.astype(np.float64))  # first m reaching D = searchsorted
+    d = np.arange(steps, dtype=np.float32) * np.float32(0.0625) - np.float32(4.0)
+    e1 = ora.expf_array(-(d - np.float32(2.0**-12)))
+    uu = ora.expf_array(-e1)
+    floors = np.maximum(np.floor(uu * np.float32(8388608.0)) - np.float32(64.0), 0).astype(np.int64)
+    noise_max = float(noise.max())
+    floors = np.where(d.astype(np.float64) > noise_max, 1 << 23, floors)
+    first = np.searchsorted(reach, d.astype(np.float64), side="left")  # 2^23 when no m reaches D_k
+    assert (floors <= first).all()
+    # Tight enough to matter: within 1024 of the exact first m (of 2^23).
+    assert ((first - floors) <= 1024).all()
+    assert d[-1] > noise_max
+
+
 def test_logf_is_faithful_on_random_positive_normals():
     rng = np.random.default_rng(1)
     bits = rng.integers(0x00800000, 0x7F800000, size=2_000_000, dtype=np.uint32)
