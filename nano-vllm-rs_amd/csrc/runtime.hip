@@ -82,6 +82,10 @@ int nv_create(int device, nv_context** output) {
     error = nvr::blas_status(hipblasCreate(&c->blas), "hipblasCreate");
     if (error) { (void)hipStreamDestroy(c->stream); delete c; return error; }
     error = nvr::blas_status(hipblasSetStream(c->blas, c->stream), "hipblasSetStream");
+    // No atomics: every GEMM gives the same bits on every run, as the
+    // reference's cuBLAS GEMMs do (graph replays equal eager launches).
+    if (!error) error = nvr::blas_status(hipblasSetAtomicsMode(c->blas, HIPBLAS_ATOMICS_NOT_ALLOWED),
+                                         "hipblasSetAtomicsMode");
     if (error) { hipblasDestroy(c->blas); (void)hipStreamDestroy(c->stream); delete c; return error; }
     *output = c;
     return 0;

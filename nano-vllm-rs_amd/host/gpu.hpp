@@ -44,6 +44,7 @@ struct Allocation;
 
 class Buffer {
 public:
+    Buffer() = default;  // empty; holds no allocation
     std::size_t len() const { return bytes_; }
     bool empty() const { return bytes_ == 0; }
     // A checked view of `bytes` bytes at `offset`; it keeps the allocation alive.

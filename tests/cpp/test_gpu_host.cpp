@@ -12,43 +12,9 @@
 #include <vector>
 
 #include "gpu.hpp"
+#include "harness.hpp"
 
 namespace {
-
-struct Case {
-    const char* name;
-    const char* kind;
-    void (*fn)();
-};
-std::vector<Case>& registry() {
-    static std::vector<Case> cases;
-    return cases;
-}
-struct Registrar {
-    Registrar(const char* name, const char* kind, void (*fn)()) { registry().push_back({name, kind, fn}); }
-};
-struct Failure {
-    std::string what;
-};
-
-#define TEST(name, kind)                                   \
-    static void name();                                    \
-    static Registrar registrar_##name(#name, kind, name); \
-    static void name()
-#define CHECK(cond)                                                                                     \
-    do {                                                                                                \
-        if (!(cond)) throw Failure{std::string(__FILE__ ":") + std::to_string(__LINE__) + ": " #cond}; \
-    } while (0)
-#define CHECK_THROWS(expr)                                                                                  \
-    do {                                                                                                    \
-        bool thrown_ = false;                                                                               \
-        try {                                                                                               \
-            expr;                                                                                           \
-        } catch (const nvr::Error&) {                                                                       \
-            thrown_ = true;                                                                                 \
-        }                                                                                                   \
-        if (!thrown_) throw Failure{std::string(__FILE__ ":") + std::to_string(__LINE__) + ": no throw: " #expr}; \
-    } while (0)
 
 // bf16 bit patterns, round to nearest even, NaN kept quiet.
 std::vector<uint8_t> bf16(const std::vector<float>& values) {
@@ -320,29 +286,3 @@ TEST(gpu_capture_failure_leaves_the_context_usable, "gpu") {
 
 }  // namespace
 
-int main(int argc, char** argv) {
-    if (argc < 2 || (std::strcmp(argv[1], "cpu") != 0 && std::strcmp(argv[1], "gpu") != 0)) {
-        std::fprintf(stderr, "usage: %s cpu|gpu\n", argv[0]);
-        return 2;
-    }
-    int failed = 0, ran = 0;
-    for (const Case& c : registry()) {
-        if (std::strcmp(c.kind, argv[1]) != 0) continue;
-        ++ran;
-        std::printf("%s ... ", c.name);
-        std::fflush(stdout);
-        try {
-            c.fn();
-            std::printf("ok\n");
-        } catch (const Failure& f) {
-            ++failed;
-            std::printf("FAILED: %s\n", f.what.c_str());
-        } catch (const std::exception& e) {
-            ++failed;
-            std::printf("FAILED: exception: %s\n", e.what());
-        }
-        std::fflush(stdout);
-    }
-    std::printf("%d of %d passed\n", ran - failed, ran);
-    return failed == 0 && ran > 0 ? 0 : 1;
-}
