@@ -42,24 +42,29 @@ __device__ __forceinline__ void zero_row16(uint4* __restrict__ dst, int chunks, 
 }
 
 // out[r] = src[index[r]] (or zeros); rows of `hidden` bf16, `hidden % 8 == 0`.
-// Each wave copies kRowsPerWave rows: their indices arrive with one load, then
-// every chunk load of those rows is in flight before the first store.
-constexpr int kRowsPerWave = 4;
+// Each wave copies kGatherRows rows: their indices arrive with one load, then
+// every chunk load of those rows is in flight before the first store. Fewer,
+// fatter waves measured faster than more, thinner ones on MI355X (16384 rows
+// of 2 KiB: 12.5 us at 8 rows a wave, 12.9 at 4 or 16, 14.1 at 1 or 2; KV
+// writes of 4 KiB rows: 22.5 us at 16 rows a wave, 23.4 at 8, 24.5 at 4,
+// 26.3 at 1).
+constexpr int kGatherRows = 8;
+constexpr int kKvRows = 16;
 constexpr int kMaxChunksPerLane = 4;  // rows up to 64 * 4 * 8 = 2048 bf16 take the unrolled path
 
 __global__ __launch_bounds__(256) void gather_rows16(const int* __restrict__ index, const uint16_t* __restrict__ src,
                                                      uint16_t* __restrict__ out, int rows, int hidden, int src_rows) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t row0 = (int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave) * kRowsPerWave;
+    const int64_t row0 = (int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave) * kGatherRows;
     if (row0 >= rows) return;
     const int chunks = hidden / 8;
-    int idx[kRowsPerWave];
+    int idx[kGatherRows];
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) idx[r] = row0 + r < rows ? index[row0 + r] : -1;
+    for (int r = 0; r < kGatherRows; ++r) idx[r] = row0 + r < rows ? index[row0 + r] : -1;
     if (chunks <= kWave * kMaxChunksPerLane) {
-        uint4 v[kRowsPerWave][kMaxChunksPerLane];
+        uint4 v[kGatherRows][kMaxChunksPerLane];
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) {
+        for (int r = 0; r < kGatherRows; ++r) {
             const bool ok = idx[r] >= 0 && idx[r] < src_rows;
             const uint4* s = reinterpret_cast<const uint4*>(src + int64_t(ok ? idx[r] : 0) * hidden);
 #pragma unroll
@@ -70,7 +75,7 @@ __global__ __launch_bounds__(256) void gather_rows16(const int* __restrict__ ind
             }
         }
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) {
+        for (int r = 0; r < kGatherRows; ++r) {
             if (row0 + r >= rows) break;
             uint4* d = reinterpret_cast<uint4*>(out + (row0 + r) * hidden);
 #pragma unroll
@@ -81,7 +86,7 @@ __global__ __launch_bounds__(256) void gather_rows16(const int* __restrict__ ind
         }
         return;
     }
-    for (int r = 0; r < kRowsPerWave && row0 + r < rows; ++r) {
+    for (int r = 0; r < kGatherRows && row0 + r < rows; ++r) {
         uint4* dst = reinterpret_cast<uint4*>(out + (row0 + r) * hidden);
         if (idx[r] >= 0 && idx[r] < src_rows)
             copy_row16(reinterpret_cast<const uint4*>(src + int64_t(idx[r]) * hidden), dst, chunks, lane);
@@ -103,22 +108,22 @@ __global__ __launch_bounds__(256) void gather_rows_generic(const int* __restrict
 }
 
 // kc[slot[r]] = k[r], vc[slot[r]] = v[r]; each row is `width` = kvh*dim bf16.
-// kRowsPerWave rows per wave with their slots loaded together, as for gathers.
+// kKvRows rows per wave with their slots loaded together, as for gathers.
 __global__ __launch_bounds__(256) void kv_write16(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
                                                   const int* __restrict__ slots, uint16_t* __restrict__ kc,
                                                   uint16_t* __restrict__ vc, int rows, int width, int64_t capacity) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t row0 = (int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave) * kRowsPerWave;
+    const int64_t row0 = (int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave) * kKvRows;
     if (row0 >= rows) return;
     const int chunks = width / 8;
-    int slot[kRowsPerWave];
+    int slot[kKvRows];
 #pragma unroll
-    for (int r = 0; r < kRowsPerWave; ++r) slot[r] = row0 + r < rows ? slots[row0 + r] : -1;
+    for (int r = 0; r < kKvRows; ++r) slot[r] = row0 + r < rows ? slots[row0 + r] : -1;
     constexpr int U = 2;  // chunks per lane per row on the unrolled path (width <= 1024)
     if (chunks <= kWave * U) {
-        uint4 a[kRowsPerWave][U], b[kRowsPerWave][U];
+        uint4 a[kKvRows][U], b[kKvRows][U];
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) {
+        for (int r = 0; r < kKvRows; ++r) {
             const bool ok = slot[r] >= 0 && int64_t(slot[r]) < capacity;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -130,7 +135,7 @@ __global__ __launch_bounds__(256) void kv_write16(const uint16_t* __restrict__ k
             }
         }
 #pragma unroll
-        for (int r = 0; r < kRowsPerWave; ++r) {
+        for (int r = 0; r < kKvRows; ++r) {
             const bool ok = slot[r] >= 0 && int64_t(slot[r]) < capacity;
             if (!ok) continue;
 #pragma unroll
@@ -144,7 +149,7 @@ __global__ __launch_bounds__(256) void kv_write16(const uint16_t* __restrict__ k
         }
         return;
     }
-    for (int r = 0; r < kRowsPerWave && row0 + r < rows; ++r) {
+    for (int r = 0; r < kKvRows && row0 + r < rows; ++r) {
         if (slot[r] < 0 || int64_t(slot[r]) >= capacity) continue;
         const uint4* ks = reinterpret_cast<const uint4*>(k + (row0 + r) * width);
         const uint4* vs = reinterpret_cast<const uint4*>(v + (row0 + r) * width);
@@ -176,7 +181,7 @@ int launch_gather(nv_context* c, const void* index, const void* src, void* out, 
     auto s = static_cast<const uint16_t*>(src);
     auto o = static_cast<uint16_t*>(out);
     if (hidden % 8 == 0 && nvr::aligned(src, 16) && nvr::aligned(out, 16)) {
-        const unsigned blocks = unsigned((int64_t(rows) + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave));
+        const unsigned blocks = unsigned((int64_t(rows) + 4 * kGatherRows - 1) / (4 * kGatherRows));
         hipLaunchKernelGGL(gather_rows16, dim3(blocks), dim3(256), 0, c->stream, idx, s, o, rows, hidden, src_rows);
     } else {
         const unsigned blocks = unsigned((int64_t(rows) + 3) / 4);
@@ -212,7 +217,7 @@ int nv_kv_write(nv_context* c, const void* k, const void* v, const void* slots, 
     auto kc16 = static_cast<uint16_t*>(kc);
     auto vc16 = static_cast<uint16_t*>(vc);
     if (width % 8 == 0 && nvr::aligned(k, 16) && nvr::aligned(v, 16) && nvr::aligned(kc, 16) && nvr::aligned(vc, 16)) {
-        const unsigned nblocks = unsigned((int64_t(rows) + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave));
+        const unsigned nblocks = unsigned((int64_t(rows) + 4 * kKvRows - 1) / (4 * kKvRows));
         hipLaunchKernelGGL(kv_write16, dim3(nblocks), dim3(256), 0, c->stream, k16, v16, sl, kc16, vc16, rows,
                            int(width), capacity);
     } else {
