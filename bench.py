@@ -369,6 +369,21 @@ def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain, only=()):
     return cases
 
 
+def measured_traffic(case):
+    """HBM bytes per launch of `case` from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE, scaled by a copy kernel of known
+    size), or None when the summary does not list it."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "pmc_traffic.txt")
+    try:
+        for line in open(path):
+            tok = line.split()
+            if len(tok) >= 6 and tok[0] == case and tok[-3].isdigit():
+                return int(tok[-3])
+    except OSError:
+        pass
+    return None
+
+
 def run_kernel_case(gpu, hip, launches, rounds):
     """Average launch time (ms) over `rounds` passes through the rotating sets."""
     graph = gpu.capture(lambda: [f() for f in launches])
@@ -475,7 +490,7 @@ def main() -> int:
         dom = max(share, key=share.get)
         kd = kernels[shape_of[dom]]
         roofline = {"kernel": shape_of[dom], "bound": "hbm", "achieved": kd["GB/s"], "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": kd["frac"], "traffic": None}
+                    "unit": "GB/s", "frac": kd["frac"], "traffic": measured_traffic(shape_of[dom])}
 
     cpu = None
     if not args.no_cpu and not only:
