@@ -27,7 +27,11 @@ stream around the whole loop, divided by the launch count.
 The CPU baseline runs the oracle's multithreaded C restatement of the same
 step (all 28 layers, T = 8192) on the host cores.
 
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-kernels]
+`decode` reports the whole Qwen3-0.6B forward (GEMMs and attention included,
+random weights) as the C++ runner serves it: 1024 prompt tokens, then decode
+steps of 8 and 32 rows, each step one HIP graph replay (decode_bench).
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--no-kernels] [--no-decode]
 """
 from __future__ import annotations
 
@@ -35,6 +39,7 @@ import argparse
 import ctypes
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -392,6 +397,20 @@ def run_kernel_case(gpu, hip, launches, rounds):
 
 
 # -------------------------------------------------------------- CPU leg ----
+def decode_steps(sequences: int) -> dict | None:
+    """The serving step of the Qwen3 forward runner (nano-vllm-rs_amd/decode_bench,
+    C++): 1024 prompt tokens in one prefill, then 127 decode steps of
+    `sequences` rows replayed as one HIP graph each, eager launches timed too.
+    Runs as a child process (its own HIP context); None when not built."""
+    exe = os.path.join(ROOT, "nano-vllm-rs_amd", "decode_bench")
+    if not os.path.exists(exe):
+        return None
+    done = subprocess.run([exe, str(sequences), "127"], capture_output=True, text=True, timeout=300)
+    if done.returncode != 0:
+        raise RuntimeError(f"decode_bench failed: {done.stderr.strip()}")
+    return json.loads(done.stdout)
+
+
 def cpu_baseline(tokens: int, layers: int, threads: int) -> dict:
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as ora
@@ -452,6 +471,7 @@ def main() -> int:
     ap.add_argument("--tokens", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
+    ap.add_argument("--no-decode", action="store_true", help="skip the forward runner's decode-step lines")
     ap.add_argument("--kernel-rounds", type=int, default=5)
     ap.add_argument("--only", default="", help="comma-separated kernel cases to run (implies --no-cpu, skips the step)")
     args = ap.parse_args()
@@ -460,10 +480,16 @@ def main() -> int:
               "(the kernels are per-token; a data-parallel split needs no collectives).", file=sys.stderr)
         return 2
 
+    only = [k for k in args.only.split(",") if k]
+    # The runner's decode steps run first, as child processes, before this
+    # process touches the GPU.
+    decode = None
+    if not args.no_decode and not only:
+        decode = {f"{n}_sequences": decode_steps(n) for n in (8, 32)}
+
     hip = Hip()
     gpu = nvr.Gpu(0)
     fill = Filler(gpu, hip)
-    only = [k for k in args.only.split(",") if k]
     chain = Chain(gpu, fill, args.tokens, 1 if only else LAYERS)
     gpu.sync()
     ms = float("nan")
@@ -506,7 +532,7 @@ def main() -> int:
                    "tokens": args.tokens, "layers": LAYERS, "hidden": H, "intermediate": I, "q_heads": QH,
                    "kv_heads": KVH, "head_dim": D, "block_size": BS, "parallelism": "none (1 GPU)"},
         "step_GB/s": round(chain_gbs, 1), "step_hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4),
-        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels,
+        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels, "decode": decode,
     }
     print(json.dumps(line))
     return 0
