@@ -78,8 +78,10 @@ __device__ __forceinline__ int64_t phys_token(int entry, int t, int bs, int bloc
     return entry >= 0 && entry < blocks ? int64_t(entry) * bs + t % bs : int64_t(-1);
 }
 
-// Compile-time geometry of attention_ordered.
-template <int DIM, int HPB>
+// Compile-time geometry of attention_ordered. OCC trades pipeline depth for
+// occupancy (see launch_ordered): 32-token V tiles instead of 64 and three K
+// buffers instead of four.
+template <int DIM, int HPB, bool OCC>
 struct OrderedLayout {
     static_assert(DIM % 32 == 0 && DIM <= 256 && HPB * DIM <= kThreads, "shape");
     static constexpr int P = DIM / 32;                    // elements per dot chain
@@ -89,21 +91,21 @@ struct OrderedLayout {
     static constexpr int kStep = kQuads * kWaves;         // tokens per block step
     static constexpr int kKLoads = kQuads / kRowsPerLoad; // load instructions per wave step (= P)
     static constexpr int kKRow = DIM * 2 + 64;            // staged K row bytes; the pad makes quad reads conflict-free
-    static constexpr int kVTile = 8192 / DIM;             // tokens per V tile (16 KB)
-    static constexpr int kVLoads = kVTile * kPieces / kThreads;  // V loads per thread per tile (4)
+    static constexpr int kVTile = (OCC ? 4096 : 8192) / DIM;  // tokens per V tile (8 or 16 KB)
+    static constexpr int kVLoads = kVTile * kPieces / kThreads;  // V loads per thread per tile (2 or 4)
     static constexpr int kKStage = kWaves * kQuads * kKRow;
     static constexpr int kVStage = 2 * kVTile * DIM * 2;
     static constexpr int kStageBytes = kKStage > kVStage ? kKStage : kVStage;
     static_assert(kKLoads * kRowsPerLoad == kQuads && kVLoads * kThreads == kVTile * kPieces, "tiles");
 };
 
-template <int DIM, int HPB, bool POW2>
+template <int DIM, int HPB, bool POW2, bool OCC>
 __global__ __launch_bounds__(kThreads) void attention_ordered(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const int* __restrict__ positions, const int* __restrict__ seqs, const int* __restrict__ tables,
     uint16_t* __restrict__ out, int qh, int kvh, int bs, int bs_shift, int blocks, int stride, int batch,
     int max_context, int score_stride) {
-    using L = OrderedLayout<DIM, HPB>;
+    using L = OrderedLayout<DIM, HPB, OCC>;
     constexpr int P = L::P, kPieces = L::kPieces, kQuads = L::kQuads, kStep = L::kStep;
     constexpr int kRowsPerLoad = L::kRowsPerLoad, kKLoads = L::kKLoads, kKRow = L::kKRow;
     constexpr int kVTile = L::kVTile, kVLoads = L::kVLoads;
@@ -224,7 +226,19 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
         }
     };
     const int nsteps = (ctx + kStep - 1) / kStep;
-    {
+    if constexpr (OCC) {  // three buffers: two steps in flight behind the one being scored
+        uint4 kA[kKLoads], kB[kKLoads], kC[kKLoads];
+        issue(kA, 0);
+        issue(kB, 1);
+        for (int s = 0; s < nsteps; s += 3) {
+            issue(kC, s + 2);
+            score(kA, s);
+            issue(kA, s + 3);
+            if (s + 1 < nsteps) score(kB, s + 1);
+            issue(kB, s + 4);
+            if (s + 2 < nsteps) score(kC, s + 2);
+        }
+    } else {
         uint4 kA[kKLoads], kB[kKLoads], kC[kKLoads], kD[kKLoads];
         issue(kA, 0);
         issue(kB, 1);
@@ -242,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     }
 
     // ---- V prefetch (see phase 3) ----
-    // A V tile is kVTile whole token rows, 16 KB: load u of thread tid covers
+    // A V tile is kVTile whole token rows (8 or 16 KB): load u of thread tid covers
     // piece cc % kPieces of token cc / kPieces, cc = tid + 256 u. Loads are
     // unconditional; invalid tokens become -0.0 when staged, which with p = +0
     // leaves every chain value unchanged, exactly as skipping them does.
@@ -415,22 +429,43 @@ __global__ __launch_bounds__(kThreads) void attention_direct(
     }
 }
 
+template <int DIM, int HPB, bool OCC>
+void launch_layout(nv_context* c, const uint16_t* q, const uint16_t* k, const uint16_t* v, const int* p, const int* s,
+                   const int* t, uint16_t* o, int rows, int qh, int kvh, int bs, int blocks, int stride, int batch,
+                   int max_context) {
+    const int score_stride = (max_context + 3) & ~3;
+    const int table_entries = (max_context - 1) / bs + 1;
+    const size_t lds = sizeof(float) * HPB * score_stride + OrderedLayout<DIM, HPB, OCC>::kStageBytes +
+                       sizeof(int) * table_entries;
+    const dim3 grid(unsigned(rows), unsigned(qh / HPB));
+    if ((bs & (bs - 1)) == 0)
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, true, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v, p,
+                           s, t, o, qh, kvh, bs, __builtin_ctz(unsigned(bs)), blocks, stride, batch, max_context,
+                           score_stride);
+    else
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, false, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v, p,
+                           s, t, o, qh, kvh, bs, 0, blocks, stride, batch, max_context, score_stride);
+}
+
+// Blocks are (row, head group) and each walks its context serially, so when
+// there are more than two blocks per CU the occupancy layout wins (three
+// blocks per CU at 164 VGPRs and 52 KB of LDS for head dim 128 and 4096
+// positions): measured on MI355X, 1024 prefill rows 164 -> 108 us (8 x 128
+// tokens) and 457 -> 348 us (one 1024-token prompt). With at most two per CU
+// the deeper pipelines win (64 x 4096 decode: 200 vs 210 us).
 template <int DIM, int HPB>
 void launch_ordered(nv_context* c, const uint16_t* q, const uint16_t* k, const uint16_t* v, const int* p,
                     const int* s, const int* t, uint16_t* o, int rows, int qh, int kvh, int bs, int blocks,
                     int stride, int batch, int max_context) {
-    const int score_stride = (max_context + 3) & ~3;
-    const int table_entries = (max_context - 1) / bs + 1;
-    const size_t lds = sizeof(float) * HPB * score_stride + OrderedLayout<DIM, HPB>::kStageBytes +
-                       sizeof(int) * table_entries;
-    const dim3 grid(unsigned(rows), unsigned(qh / HPB));
-    if ((bs & (bs - 1)) == 0)
-        hipLaunchKernelGGL((attention_ordered<DIM, HPB, true>), grid, dim3(kThreads), lds, c->stream, q, k, v, p, s, t,
-                           o, qh, kvh, bs, __builtin_ctz(unsigned(bs)), blocks, stride, batch, max_context,
-                           score_stride);
-    else
-        hipLaunchKernelGGL((attention_ordered<DIM, HPB, false>), grid, dim3(kThreads), lds, c->stream, q, k, v, p, s,
-                           t, o, qh, kvh, bs, 0, blocks, stride, batch, max_context, score_stride);
+    if constexpr (DIM == 128 && HPB == 2) {
+        const int64_t groups = int64_t(rows) * (qh / HPB);
+        if (groups > 2 * int64_t(c->cu_count > 0 ? c->cu_count : 256)) {
+            launch_layout<DIM, HPB, true>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride, batch,
+                                          max_context);
+            return;
+        }
+    }
+    launch_layout<DIM, HPB, false>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride, batch, max_context);
 }
 
 template <int DIM>

@@ -483,6 +483,16 @@ def test_attention_ragged_prefill_rows(gpu):
     _attention_case(gpu, 210, pos, seqs, 16, 8, 128, 16, 3, 44, 1024)
 
 
+def test_attention_many_rows_odd_block_size(gpu):
+    """600 prefill rows (two 300-token prompts) with 7-token blocks: more than
+    two head-pair blocks per CU, so the occupancy layout runs, with the
+    block-size division path."""
+    lens = [300, 300]
+    pos = np.concatenate([np.arange(n) for n in lens])
+    seqs = np.concatenate([np.full(n, i) for i, n in enumerate(lens)])
+    _attention_case(gpu, 215, pos, seqs, 16, 8, 128, 7, 2, 44, 300)
+
+
 @pytest.mark.parametrize("dim,qh,kvh,bs", [(32, 4, 2, 8), (64, 8, 2, 256), (256, 4, 4, 16), (128, 6, 2, 7),
                                            (128, 4, 4, 32), (80, 4, 2, 16), (96, 2, 1, 5), (2, 2, 2, 4)])
 def test_attention_head_dims_groups_and_block_sizes(gpu, dim, qh, kvh, bs):
