@@ -284,16 +284,27 @@ __global__ __launch_bounds__(256) void sample_refine(const uint16_t* __restrict_
 }
 
 // ------------------------------------------------------ row-resident ----
+// Threads per resident block; a row takes 1024 / kResThreads blocks. Two
+// 512-thread blocks per row (halves folded by sample_combine; parity-tested)
+// measured slower at 256 rows of 151936 on MI355X: greedy 20.1 vs 15.9 us,
+// T = 0.6 52.4 vs 37.6 us (each half prunes against its own, weaker s0),
+// half and half 40.8 vs 37.2 us.
 constexpr int kResThreads = 1024;
-constexpr int kResWaves = kResThreads / kWave;
-constexpr int kResMaxChunks = 20;  // 16-byte chunks per lane: vocab <= 20 * 8192
-constexpr int kResQueue = 2432;    // candidate entries per wave: the 16 queues take 152 KiB of LDS
+constexpr int kResMaxChunks = 20;  // 16-byte chunks per lane: a part holds at most 20 * 8 * TPB tokens
 constexpr int kXFloors = 1024;     // tabulated per-logit hash floors (see sample_resident)
 // Noise thresholds at D_k = -4 + k/16, k < kFloorSteps; the last lies above kNoiseMax.
 constexpr int kFloorSteps = 336;
-constexpr size_t kResLdsBytes = sizeof(uint32_t) * (size_t(kResWaves) * kResQueue + kFloorSteps + kXFloors) +
-                                3 * kResWaves * (sizeof(float) + sizeof(int));
-static_assert(kResLdsBytes <= 160 * 1024, "the row-resident sampler's LDS must fit one CU");
+// Block geometry: TPB threads per block (1024: one block per CU holding a
+// whole row; 512: two blocks per CU, each holding half a row). Candidate
+// queues per wave fill the block's share of the CU's 160 KiB of LDS.
+template <int TPB>
+struct ResGeometry {
+    static constexpr int kWaves = TPB / kWave;
+    static constexpr int kQueue = TPB == 1024 ? 2432 : 2304;
+    static constexpr size_t kLdsBytes = sizeof(uint32_t) * (size_t(kWaves) * kQueue + kFloorSteps + kXFloors) +
+                                        3 * kWaves * (sizeof(float) + sizeof(int));
+    static_assert(kLdsBytes * (1024 / TPB) <= 160 * 1024, "the resident sampler's blocks must fit one CU's LDS");
+};
 
 // Lower bound of the hash values whose Gumbel noise -ln(-ln(u)) reaches D_k:
 // every m (the top 23 hash bits) with noise(m) >= D_k has m >= noise_floor(k).
@@ -343,17 +354,18 @@ __device__ __forceinline__ float score_from_m(float logit, float temperature, ui
 
 // Scores a wave's queue entries [lane, count), two per lane per iteration (an
 // odd tail scores one entry twice). Entry = f32 bits of the logit (low 16 bits
-// zero) | chunk round k << 9 | lane << 3 | element, for the wave whose first
-// lane is `base`. TAB: the hash floor of a logit is read from xfloors, indexed
-// by its bf16 bits minus lxb, instead of computed.
+// zero) | chunk round k << 9 | lane << 3 | element; chunk = k * stride + base +
+// lane, base being the wave's first chunk of round 0. TAB: the hash floor of a
+// logit is read from xfloors, indexed by its bf16 bits minus lxb, instead of
+// computed.
 template <bool TAB>
-__device__ __forceinline__ void score_queue(const uint32_t* queue, int count, int lane, int base, const Pruner& p,
-                                            const uint32_t* xfloors, int lxb, Best& best) {
+__device__ __forceinline__ void score_queue(const uint32_t* queue, int count, int lane, int base, int stride,
+                                            const Pruner& p, const uint32_t* xfloors, int lxb, Best& best) {
     for (int j = lane; j < count; j += 2 * kWave) {
         const uint32_t e0 = queue[j];
         const uint32_t e1 = queue[j + kWave < count ? j + kWave : j];
-        const int ta = 8 * (int(e0 >> 9 & 31u) * kResThreads + base + int(e0 >> 3 & 63u)) + int(e0 & 7u);
-        const int tb = 8 * (int(e1 >> 9 & 31u) * kResThreads + base + int(e1 >> 3 & 63u)) + int(e1 & 7u);
+        const int ta = 8 * (int(e0 >> 9 & 31u) * stride + base + int(e0 >> 3 & 63u)) + int(e0 & 7u);
+        const int tb = 8 * (int(e1 >> 9 & 31u) * stride + base + int(e1 >> 3 & 63u)) + int(e1 & 7u);
         const float xa = __uint_as_float(e0 & 0xffff0000u), xb = __uint_as_float(e1 & 0xffff0000u);
         // Floors first, both hashes interleaved, one rare branch each.
         const uint32_t fa = TAB ? xfloors[int(e0 >> 16) - lxb] : hash_floor(p, xa);
@@ -367,8 +379,9 @@ __device__ __forceinline__ void score_queue(const uint32_t* queue, int count, in
     }
 }
 
-// Argmax over the 1024-thread block; the result is valid in every thread.
-// Each call needs its own kResWaves slots in `scores` / `ids`.
+// Argmax over a block of W waves; the result is valid in every thread. Each
+// call needs its own W slots in `scores` / `ids`.
+template <int W>
 __device__ __forceinline__ Best block_fold(Best b, float* scores, int* ids) {
     b = wave_argmax(b);
     if ((threadIdx.x & (kWave - 1)) == 0) {
@@ -378,15 +391,17 @@ __device__ __forceinline__ Best block_fold(Best b, float* scores, int* ids) {
     __syncthreads();
     Best r{scores[0], ids[0]};
 #pragma unroll
-    for (int w = 1; w < kResWaves; ++w) consider(r, scores[w], ids[w]);
+    for (int w = 1; w < W; ++w) consider(r, scores[w], ids[w]);
     return r;
 }
 
-// One row per 1024-thread block, the row resident in registers: lane t of the
-// block holds chunks t, t + 1024, ... (C of them) of 8 logits, all loads issued
-// first. Phase 1 (as the chunks arrive): the lane's greedy maximum. Greedy rows
+// One row (parts == 1) or one half of a row (parts == 2) per block, resident
+// in registers: lane t of part p holds chunks k * parts * TPB + p * TPB + t
+// (k < C) of 8 logits, all loads issued first. A whole row writes out[row];
+// a half writes its (score, index) to the partials, for sample_combine. Phase 1 (as the chunks arrive): the lane's greedy maximum. Greedy rows
 // end with the block's maximum. Gumbel rows: every lane scores its maximum's
-// token exactly; the best of those 1024 real scores is s0. A token whose
+// token exactly; the best of those real scores (of this part) is s0, a lower
+// bound for the part's own winner. A token whose
 // logit * (1/T) is below E = (s0 - kNoiseMax) - (|s0| + 34) * 2^-17 cannot
 // reach s0 (the noise never exceeds kNoiseMax; the margin covers 1/T's and the
 // score's roundings), so each wave compacts the others into its LDS queue
@@ -397,29 +412,44 @@ __device__ __forceinline__ Best block_fold(Best b, float* scores, int* ids) {
 // logit costs the whole batch about 1 us (151936 logits / 64 lanes per
 // wave-instruction at one wave-instruction per cycle per CU); the compaction
 // is therefore kept at a handful of instructions per logit.
-template <int C>
-__global__ __launch_bounds__(kResThreads) void sample_resident(const uint16_t* __restrict__ logits,
-                                                               const float* __restrict__ temps,
-                                                               const uint64_t* __restrict__ seeds,
-                                                               int* __restrict__ out, int vocab) {
+template <int C, int TPB>
+__global__ __launch_bounds__(TPB) void sample_resident(const uint16_t* __restrict__ logits,
+                                                       const float* __restrict__ temps,
+                                                       const uint64_t* __restrict__ seeds, int* __restrict__ out,
+                                                       float* __restrict__ partial_scores,
+                                                       int* __restrict__ partial_ids, int vocab, int parts,
+                                                       int partial_stride) {
+    using G = ResGeometry<TPB>;
+    constexpr int kW = G::kWaves, kQ = G::kQueue;
     extern __shared__ __align__(16) uint32_t lds[];
-    uint32_t* floors = lds + kResWaves * kResQueue;
+    uint32_t* floors = lds + kW * kQ;
     uint32_t* xfloors = floors + kFloorSteps;
     float* fold_s = reinterpret_cast<float*>(xfloors + kXFloors);
-    int* fold_i = reinterpret_cast<int*>(fold_s + 3 * kResWaves);
+    int* fold_i = reinterpret_cast<int*>(fold_s + 3 * kW);
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int r = blockIdx.x;
+    const int r = blockIdx.x / parts, part = blockIdx.x - r * parts;
     const int chunks = vocab / 8;
+    const int stride = parts * TPB;       // chunks between a lane's rounds
+    const int first = part * TPB + tid;   // the lane's round-0 chunk
     const uint16_t* row = logits + int64_t(r) * vocab;
+    auto finish = [&](const Best& b) {
+        if (tid != 0) return;
+        if (parts == 1) {
+            out[r] = b.index == nvr::kNoIndex ? 0 : b.index;
+        } else {
+            partial_scores[int64_t(r) * partial_stride + part] = b.score;
+            partial_ids[int64_t(r) * partial_stride + part] = b.index;
+        }
+    };
 
     uint4 w[C];
 #pragma unroll
-    for (int k = 0; k < C; ++k) w[k] = nvr::load_stream(row + 8 * int64_t(min(k * kResThreads + tid, chunks - 1)));
+    for (int k = 0; k < C; ++k) w[k] = nvr::load_stream(row + 8 * int64_t(min(k * stride + first, chunks - 1)));
     const float temperature = temps[r];
     const uint64_t seed = seeds[r];
     const bool gumbel = temperature > 0.0f;
     if (gumbel)
-        for (int k = tid; k < kFloorSteps; k += kResThreads) floors[k] = noise_floor(k);
+        for (int k = tid; k < kFloorSteps; k += TPB) floors[k] = noise_floor(k);
 
     // Phase 1, as the chunks arrive: the lane's best chunk under "higher
     // maximum wins; an equal maximum only while there is none" (the lane sees
@@ -431,7 +461,7 @@ __global__ __launch_bounds__(kResThreads) void sample_resident(const uint16_t* _
     int bk = -1;
 #pragma unroll
     for (int k = 0; k < C; ++k) {
-        const bool valid = k * kResThreads + tid < chunks;
+        const bool valid = k * stride + first < chunks;
         w[k].x = valid ? w[k].x : kNaN2;
         w[k].y = valid ? w[k].y : kNaN2;
         w[k].z = valid ? w[k].z : kNaN2;
@@ -460,23 +490,23 @@ __global__ __launch_bounds__(kResThreads) void sample_resident(const uint16_t* _
         int e = 8;
 #pragma unroll
         for (int i = 7; i >= 0; --i) e = f[i] == bv ? i : e;
-        if (bk >= 0) lb.index = 8 * (bk * kResThreads + tid) + e;
+        if (bk >= 0) lb.index = 8 * (bk * stride + first) + e;
     }
     // Keep only the packed words live into phase 3 (without this the compiler
     // keeps phase 1's unpacked floats instead, twice the registers).
 #pragma unroll
     for (int k = 0; k < C; ++k) __asm__ volatile("" : "+v"(w[k].x), "+v"(w[k].y), "+v"(w[k].z), "+v"(w[k].w));
-    const Best top = block_fold(lb, fold_s, fold_i);
+    const Best top = block_fold<kW>(lb, fold_s, fold_i);
     if (!gumbel) {
-        if (tid == 0) out[r] = top.index == nvr::kNoIndex ? 0 : top.index;
+        finish(top);
         return;
     }
 
     // Phase 2: s0 from the lanes' maxima (each the score of a real token).
     Best own{-__builtin_inff(), nvr::kNoIndex};
     if (lb.index != nvr::kNoIndex) own = Best{nvr::gumbel_score(lb.score, temperature, seed, uint32_t(lb.index)), lb.index};
-    const Best first = block_fold(own, fold_s + kResWaves, fold_i + kResWaves);
-    const float s0 = first.score, inv_t = 1.0f / temperature;
+    const Best seeded = block_fold<kW>(own, fold_s + kW, fold_i + kW);
+    const float s0 = seeded.score, inv_t = 1.0f / temperature;
     const bool on = __builtin_fabsf(s0) < __builtin_inff() && inv_t < __builtin_inff();
     const float bound = on ? (s0 - kNoiseMax) - (__builtin_fabsf(s0) + 34.0f) * 0x1.0p-17f : -__builtin_inff();
     // The candidates are exactly the logits x >= lx, lx the smallest bf16 value
@@ -496,17 +526,17 @@ __global__ __launch_bounds__(kResThreads) void sample_resident(const uint16_t* _
     }
 
     // Phase 3: each wave compacts its candidates into its LDS queue (ballot +
-    // mbcnt) and scores them, in rounds of kResQueue entries when there are
+    // mbcnt) and scores them, in rounds of kQ entries when there are
     // more (a round re-runs the compaction from the registers and keeps the
     // next window). Entry = f32 bits of the logit (low 16 bits zero) | chunk
     // round k << 9 | lane << 3 | element. Chunks past the row end are NaN and
     // never candidates. The counts vary between rows far more than between
     // the waves of a row (measured), so each wave scores its own queue.
-    uint32_t* queue = lds + wave * kResQueue;
+    uint32_t* queue = lds + wave * kQ;
     const uint32_t lane_code = uint32_t(lane) << 3;
-    const int base = wave * kWave;
+    const int base = part * TPB + wave * kWave;
     const Pruner p{s0, inv_t, temperature, seed, on, floors};
-    Best best = first;
+    Best best = seeded;
     // When every candidate is positive (lx > 0) and the candidates span at
     // most kXFloors bf16 values (lx up to the row maximum), hash_floor is
     // tabulated once per value (a few hundred at low temperatures) instead of
@@ -515,10 +545,10 @@ __global__ __launch_bounds__(kResThreads) void sample_resident(const uint16_t* _
     const int span = (on & (lx > 0.0f) & (top.score >= lx)) ? int(__float_as_uint(top.score) >> 16) - lxb + 1 : 0;
     const bool tab = span > 0 && span <= kXFloors;
     if (tab) {
-        for (int j = tid; j < span; j += kResThreads) xfloors[j] = hash_floor(p, nvr::bf16_to_f32(uint16_t(lxb + j)));
+        for (int j = tid; j < span; j += TPB) xfloors[j] = hash_floor(p, nvr::bf16_to_f32(uint16_t(lxb + j)));
         __syncthreads();
     }
-    for (int window = 0;; window += kResQueue) {
+    for (int window = 0;; window += kQ) {
         int n = -window;  // queue position of the next candidate
 #pragma unroll
         for (int k = 0; k < C; ++k) {
@@ -533,17 +563,17 @@ __global__ __launch_bounds__(kResThreads) void sample_resident(const uint16_t* _
                 const uint64_t ballot = __ballot(take);
                 const uint32_t pos = __builtin_amdgcn_mbcnt_hi(uint32_t(ballot >> 32),
                                                                __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), uint32_t(n)));
-                if (take & (pos < uint32_t(kResQueue))) queue[pos] = xb | lane_code | uint32_t(k << 9 | i);
+                if (take & (pos < uint32_t(kQ))) queue[pos] = xb | lane_code | uint32_t(k << 9 | i);
                 n += int(__popcll(ballot));
             }
         }
-        if (window == 0 && n > 2 * kResQueue) {
+        if (window == 0 && n > 2 * kQ) {
             // Most tokens are candidates (high temperature, flat rows): queue
             // rounds would cost more than they save, so every lane scores its
             // own candidates, re-reading its chunks (cache hits).
             const uint32_t* words = reinterpret_cast<const uint32_t*>(row);
 #pragma unroll 1
-            for (int c = tid; c < chunks; c += kResThreads) {
+            for (int c = first; c < chunks; c += stride) {
                 const uint4 v = *reinterpret_cast<const uint4*>(words + 4 * c);
                 const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -560,16 +590,16 @@ __global__ __launch_bounds__(kResThreads) void sample_resident(const uint16_t* _
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int count = min(n, kResQueue);
-        if (tab) score_queue<true>(queue, count, lane, base, p, xfloors, lxb, best);
-        else score_queue<false>(queue, count, lane, base, p, xfloors, lxb, best);
-        if (n <= kResQueue) break;
+        const int count = min(n, kQ);
+        if (tab) score_queue<true>(queue, count, lane, base, stride, p, xfloors, lxb, best);
+        else score_queue<false>(queue, count, lane, base, stride, p, xfloors, lxb, best);
+        if (n <= kQ) break;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    best = block_fold(best, fold_s + 2 * kResWaves, fold_i + 2 * kResWaves);
-    if (tid == 0) out[r] = best.index == nvr::kNoIndex ? 0 : best.index;
+    best = block_fold<kW>(best, fold_s + 2 * kW, fold_i + 2 * kW);
+    finish(best);
 }
 
 // Generic partitions (unaligned rows or vocab % 8 != 0): 2048-token
@@ -621,6 +651,26 @@ int launch_serial(nv_context* c, const void* logits, const void* temps, const vo
     return nvr::launch_status();
 }
 
+template <int TPB>
+int launch_resident(nv_context* c, const uint16_t* logits, const float* temps, const uint64_t* seeds, int* out,
+                    float* partial_scores, int* partial_ids, int batch, int vocab, int chunks_per_lane) {
+    constexpr int parts = 1024 / TPB;
+    const dim3 grid(unsigned(batch * parts)), block(TPB);
+    const size_t lds = ResGeometry<TPB>::kLdsBytes;
+    switch (chunks_per_lane) {
+    case 4: hipLaunchKernelGGL((sample_resident<4, TPB>), grid, block, lds, c->stream, logits, temps, seeds, out, partial_scores, partial_ids, vocab, parts, parts); break;
+    case 8: hipLaunchKernelGGL((sample_resident<8, TPB>), grid, block, lds, c->stream, logits, temps, seeds, out, partial_scores, partial_ids, vocab, parts, parts); break;
+    case 12: hipLaunchKernelGGL((sample_resident<12, TPB>), grid, block, lds, c->stream, logits, temps, seeds, out, partial_scores, partial_ids, vocab, parts, parts); break;
+    case 16: hipLaunchKernelGGL((sample_resident<16, TPB>), grid, block, lds, c->stream, logits, temps, seeds, out, partial_scores, partial_ids, vocab, parts, parts); break;
+    default: hipLaunchKernelGGL((sample_resident<20, TPB>), grid, block, lds, c->stream, logits, temps, seeds, out, partial_scores, partial_ids, vocab, parts, parts); break;
+    }
+    if (parts == 1) return nvr::launch_status();
+    NVR_HIP(hipGetLastError());
+    hipLaunchKernelGGL(sample_combine, dim3(unsigned(batch)), dim3(64), 0, c->stream, partial_scores, partial_ids, out,
+                       parts);
+    return nvr::launch_status();
+}
+
 }  // namespace
 
 extern "C" {
@@ -644,23 +694,15 @@ int nv_sample_parallel(nv_context* c, const void* logits, const void* temps, con
     auto s = static_cast<const uint64_t*>(seeds);
     auto ps = static_cast<float*>(partial_scores);
     auto pi = static_cast<int*>(partial_ids);
-    const int64_t lane_chunks = (int64_t(vocab) / 8 + kResThreads - 1) / kResThreads;
     // One row per CU: worth it once every CU has a row (measured at 256 rows
     // of 151936 on MI355X: greedy 16 vs 23 us, T = 0.6 39 vs 51 us, half and
     // half 38 vs 40 us, T = 1 76 vs 86 us; with 192 rows the partitions win
     // mixed and T = 1 batches).
     const int min_rows = c->cu_count > 0 ? c->cu_count : 256;
-    if (batch >= min_rows && vector_rows(logits, vocab) && lane_chunks <= kResMaxChunks) {
-        auto o = static_cast<int*>(out);
-        switch ((lane_chunks + 3) / 4) {
-        case 1: hipLaunchKernelGGL(sample_resident<4>, dim3(batch), dim3(kResThreads), kResLdsBytes, c->stream, l16, t, s, o, vocab); break;
-        case 2: hipLaunchKernelGGL(sample_resident<8>, dim3(batch), dim3(kResThreads), kResLdsBytes, c->stream, l16, t, s, o, vocab); break;
-        case 3: hipLaunchKernelGGL(sample_resident<12>, dim3(batch), dim3(kResThreads), kResLdsBytes, c->stream, l16, t, s, o, vocab); break;
-        case 4: hipLaunchKernelGGL(sample_resident<16>, dim3(batch), dim3(kResThreads), kResLdsBytes, c->stream, l16, t, s, o, vocab); break;
-        default: hipLaunchKernelGGL(sample_resident<20>, dim3(batch), dim3(kResThreads), kResLdsBytes, c->stream, l16, t, s, o, vocab); break;
-        }
-        return nvr::launch_status();
-    }
+    const int64_t lane_chunks = (int64_t(vocab) / 8 + 1023) / 1024;  // per lane of the row's 1024 threads
+    if (batch >= min_rows && vector_rows(logits, vocab) && lane_chunks <= kResMaxChunks)
+        return launch_resident<kResThreads>(c, l16, t, s, static_cast<int*>(out), ps, pi, batch, vocab,
+                                            int((lane_chunks + 3) / 4 * 4));
     int parts;
     if (vector_rows(logits, vocab)) {
         // Never more partitions than the scratch holds (ceil(vocab / 2048)).
