@@ -99,7 +99,12 @@ struct OrderedLayout {
     static_assert(kKLoads * kRowsPerLoad == kQuads && kVLoads * kThreads == kVTile * kPieces, "tiles");
 };
 
-template <int DIM, int HPB, bool POW2, bool OCC>
+// How a logical token finds its physical row: kAnyBs divides by the block
+// size; kPow2 shifts (bs a power of two); kAligned (bs a power of two holding
+// whole K steps and V tiles) looks the block entry up once per step or tile.
+constexpr int kAnyBs = 0, kPow2 = 1, kAligned = 2;
+
+template <int DIM, int HPB, int TABLE, bool OCC>
 __global__ __launch_bounds__(kThreads) void attention_ordered(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const int* __restrict__ positions, const int* __restrict__ seqs, const int* __restrict__ tables,
@@ -140,14 +145,19 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
         __syncthreads();
     }
     // Physical token row (block * bs + offset) of logical token t < ctx, or -1
-    // for an invalid block. The host guarantees blocks * bs fits in int32, and
-    // POW2 (bs a power of two) turns the division into a shift.
+    // for an invalid block. The host guarantees blocks * bs fits in int32.
+    constexpr bool kShift = TABLE != kAnyBs;
     auto phys = [&](int t) -> int {
-        const int lb = POW2 ? t >> bs_shift : t / bs;
-        const int off = POW2 ? t & (bs - 1) : t - lb * bs;
+        const int lb = kShift ? t >> bs_shift : t / bs;
+        const int off = kShift ? t & (bs - 1) : t - lb * bs;
         const int e = ltable[lb];
         return e >= 0 && e < blocks ? e * bs + off : -1;
     };
+    // kAligned: the block entry of the aligned group (a K step or a V tile)
+    // that starts at logical token t0, clamped into the context, and the
+    // physical row of a token t of that group (-1 for an invalid block).
+    auto group_entry = [&](int t0) -> int { return ltable[min(t0, ctx - 1) >> bs_shift]; };
+    auto phys_in = [&](int e, int t) -> int { return e >= 0 && e < blocks ? e * bs + (t & (bs - 1)) : -1; };
 
     // ---- 1. scores ----
     // Loads read whole rows: load instruction k of a wave step gives lane l
@@ -179,10 +189,11 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     // token 0 of block 0 and its dot is discarded), so no branch makes the
     // compiler drain the load queue.
     auto issue = [&](uint4 (&kb)[kKLoads], int s) {
+        const int e = TABLE == kAligned ? group_entry(s * kStep) : 0;
 #pragma unroll
         for (int k = 0; k < kKLoads; ++k) {
             const int t = s * kStep + wave * kQuads + k * kRowsPerLoad + lrow;
-            const int ph = phys(min(t, ctx - 1));
+            const int ph = TABLE == kAligned ? phys_in(e, t) : phys(min(t, ctx - 1));
             kb[k] = nvr::load_stream(kcol + int64_t(t < ctx && ph >= 0 ? ph : 0) * token_stride);
         }
     };
@@ -201,7 +212,8 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
             nvr::unpack8(*reinterpret_cast<const uint4*>(krows + tq * kKRow + 16 * (4 * j + a)), kf[j]);
         const int t = s * kStep + wave * kQuads + tq;
         const bool live = t < ctx;
-        const bool valid = live && phys(min(t, ctx - 1)) >= 0;
+        const bool valid = live && (TABLE == kAligned ? phys_in(group_entry(s * kStep), t)
+                                                      : phys(min(t, ctx - 1))) >= 0;
 #pragma unroll
         for (int g = 0; g < HPB; ++g) {
             float acc[8];
@@ -262,11 +274,12 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     // leaves every chain value unchanged, exactly as skipping them does.
     const uint16_t* vcol = vc + int64_t(kvhead) * DIM;
     auto load_vtile = [&](uint4 (&r)[kVLoads], bool (&ok)[kVLoads], int t0) {
+        const int e = TABLE == kAligned ? group_entry(t0) : 0;
 #pragma unroll
         for (int u = 0; u < kVLoads; ++u) {
             const int cc = int(threadIdx.x) + kThreads * u;
             const int t = t0 + cc / kPieces;
-            const int ph = phys(min(t, ctx - 1));
+            const int ph = TABLE == kAligned ? phys_in(e, t) : phys(min(t, ctx - 1));
             ok[u] = t < ctx && ph >= 0;
             r[u] = nvr::load_stream(vcol + int64_t(ok[u] ? ph : 0) * token_stride + 8 * (cc % kPieces));
         }
@@ -322,8 +335,7 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
         const int n = min(kVTile, ctx - t0);
         if (!chain || n <= 0) return;
         const uint16_t* vt = slots + slot * kVTile * DIM + d;
-        int j = 0;
-        for (; j + 8 <= n; j += 8) {
+        auto eight = [&](int j) {
             const float4 p0 = *reinterpret_cast<const float4*>(pg + t0 + j);
             const float4 p1 = *reinterpret_cast<const float4*>(pg + t0 + j + 4);
             float v[8];
@@ -337,7 +349,16 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
             acc = __builtin_fmaf(p1.y, v[5], acc);
             acc = __builtin_fmaf(p1.z, v[6], acc);
             acc = __builtin_fmaf(p1.w, v[7], acc);
+        };
+        if (n == kVTile) {
+            // A whole tile, unrolled, so the LDS reads of later tokens are
+            // issued ahead of the chain instead of one round trip per 8 tokens.
+#pragma unroll
+            for (int j = 0; j < kVTile; j += 8) eight(j);
+            return;
         }
+        int j = 0;
+        for (; j + 8 <= n; j += 8) eight(j);
         for (; j < n; ++j) acc = __builtin_fmaf(pg[t0 + j], nvr::bf16_to_f32(vt[j * DIM]), acc);
     };
     // Three register tiles in fixed roles keep two tiles in flight while one
@@ -437,14 +458,19 @@ void launch_layout(nv_context* c, const uint16_t* q, const uint16_t* k, const ui
     const int table_entries = (max_context - 1) / bs + 1;
     const size_t lds = sizeof(float) * HPB * score_stride + OrderedLayout<DIM, HPB, OCC>::kStageBytes +
                        sizeof(int) * table_entries;
+    using L = OrderedLayout<DIM, HPB, OCC>;
     const dim3 grid(unsigned(rows), unsigned(qh / HPB));
-    if ((bs & (bs - 1)) == 0)
-        hipLaunchKernelGGL((attention_ordered<DIM, HPB, true, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v, p,
-                           s, t, o, qh, kvh, bs, __builtin_ctz(unsigned(bs)), blocks, stride, batch, max_context,
-                           score_stride);
+    const bool pow2 = (bs & (bs - 1)) == 0;
+    const int shift = pow2 ? __builtin_ctz(unsigned(bs)) : 0;
+    if (pow2 && bs >= L::kStep && bs >= L::kVTile)
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAligned, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v,
+                           p, s, t, o, qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride);
+    else if (pow2)
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kPow2, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v, p,
+                           s, t, o, qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride);
     else
-        hipLaunchKernelGGL((attention_ordered<DIM, HPB, false, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v, p,
-                           s, t, o, qh, kvh, bs, 0, blocks, stride, batch, max_context, score_stride);
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAnyBs, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v,
+                           p, s, t, o, qh, kvh, bs, 0, blocks, stride, batch, max_context, score_stride);
 }
 
 // Blocks are (row, head group) and each walks its context serially, so when
