@@ -136,11 +136,15 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     const int ctx = int(context64);
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int64_t token_stride = int64_t(kvh) * DIM;  // elements between consecutive tokens of a block
-    // The row's block-table entries go to LDS once, so K/V addresses depend on
-    // LDS reads only and the global loads can stay queued.
-    {
-        const int* table = tables + int64_t(seq) * stride;
-        const int nent = (ctx - 1) / bs + 1;
+    // The row's block-table entries: with kAligned (at most 64 entries) lane i
+    // of every wave holds entry i, read back with readlane; otherwise they go
+    // to LDS once. Either way K/V addresses never wait on a global load.
+    const int* table = tables + int64_t(seq) * stride;
+    const int nent = (ctx - 1) / bs + 1;
+    int lane_entry = -1;
+    if constexpr (TABLE == kAligned) {
+        if (lane < nent) lane_entry = table[lane];
+    } else {
         for (int i = threadIdx.x; i < nent; i += kThreads) ltable[i] = table[i];
         __syncthreads();
     }
@@ -154,10 +158,18 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
         return e >= 0 && e < blocks ? e * bs + off : -1;
     };
     // kAligned: the block entry of the aligned group (a K step or a V tile)
-    // that starts at logical token t0, clamped into the context, and the
-    // physical row of a token t of that group (-1 for an invalid block).
-    auto group_entry = [&](int t0) -> int { return ltable[min(t0, ctx - 1) >> bs_shift]; };
-    auto phys_in = [&](int e, int t) -> int { return e >= 0 && e < blocks ? e * bs + (t & (bs - 1)) : -1; };
+    // that starts at logical token t0 (clamped into the context; uniform),
+    // whether it is a valid block, and the address of the group's first token
+    // row in `col` (block 0 for an invalid entry, so that every load of the
+    // group stays inside an allocated block; its data is then discarded).
+    auto group_entry = [&](int t0) -> int {
+        return __builtin_amdgcn_readlane(lane_entry, min(t0, ctx - 1) >> bs_shift);
+    };
+    auto entry_ok = [&](int e) { return e >= 0 && e < blocks; };
+    auto group_base = [&](const uint16_t* col, int e, int t0) {
+        return col + (entry_ok(e) ? int64_t(e) * bs * token_stride : int64_t(0)) +
+               int64_t(t0 & (bs - 1)) * token_stride;
+    };
 
     // ---- 1. scores ----
     // Loads read whole rows: load instruction k of a wave step gives lane l
@@ -188,13 +200,21 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     // are unconditional (a token past the context or in an invalid block reads
     // token 0 of block 0 and its dot is discarded), so no branch makes the
     // compiler drain the load queue.
+    // kAligned: lane offsets of a step's rows from the step's first row.
+    const int klane = (wave * kQuads + lrow) * int(token_stride);
     auto issue = [&](uint4 (&kb)[kKLoads], int s) {
-        const int e = TABLE == kAligned ? group_entry(s * kStep) : 0;
+        if constexpr (TABLE == kAligned) {
+            const uint16_t* base = group_base(kcol, group_entry(s * kStep), s * kStep);
 #pragma unroll
-        for (int k = 0; k < kKLoads; ++k) {
-            const int t = s * kStep + wave * kQuads + k * kRowsPerLoad + lrow;
-            const int ph = TABLE == kAligned ? phys_in(e, t) : phys(min(t, ctx - 1));
-            kb[k] = nvr::load_stream(kcol + int64_t(t < ctx && ph >= 0 ? ph : 0) * token_stride);
+            for (int k = 0; k < kKLoads; ++k)
+                kb[k] = nvr::load_stream(base + klane + k * kRowsPerLoad * int(token_stride));
+        } else {
+#pragma unroll
+            for (int k = 0; k < kKLoads; ++k) {
+                const int t = s * kStep + wave * kQuads + k * kRowsPerLoad + lrow;
+                const int ph = phys(min(t, ctx - 1));
+                kb[k] = nvr::load_stream(kcol + int64_t(t < ctx && ph >= 0 ? ph : 0) * token_stride);
+            }
         }
     };
     auto score = [&](const uint4 (&kb)[kKLoads], int s) {
@@ -212,8 +232,8 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
             nvr::unpack8(*reinterpret_cast<const uint4*>(krows + tq * kKRow + 16 * (4 * j + a)), kf[j]);
         const int t = s * kStep + wave * kQuads + tq;
         const bool live = t < ctx;
-        const bool valid = live && (TABLE == kAligned ? phys_in(group_entry(s * kStep), t)
-                                                      : phys(min(t, ctx - 1))) >= 0;
+        const bool valid = live && (TABLE == kAligned ? entry_ok(group_entry(s * kStep))
+                                                      : phys(min(t, ctx - 1)) >= 0);
 #pragma unroll
         for (int g = 0; g < HPB; ++g) {
             float acc[8];
@@ -274,14 +294,24 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     // leaves every chain value unchanged, exactly as skipping them does.
     const uint16_t* vcol = vc + int64_t(kvhead) * DIM;
     auto load_vtile = [&](uint4 (&r)[kVLoads], bool (&ok)[kVLoads], int t0) {
-        const int e = TABLE == kAligned ? group_entry(t0) : 0;
+        if constexpr (TABLE == kAligned) {
+            const int e = group_entry(t0);
+            const uint16_t* base = group_base(vcol, e, t0);
 #pragma unroll
-        for (int u = 0; u < kVLoads; ++u) {
-            const int cc = int(threadIdx.x) + kThreads * u;
-            const int t = t0 + cc / kPieces;
-            const int ph = TABLE == kAligned ? phys_in(e, t) : phys(min(t, ctx - 1));
-            ok[u] = t < ctx && ph >= 0;
-            r[u] = nvr::load_stream(vcol + int64_t(ok[u] ? ph : 0) * token_stride + 8 * (cc % kPieces));
+            for (int u = 0; u < kVLoads; ++u) {
+                const int cc = int(threadIdx.x) + kThreads * u;
+                ok[u] = entry_ok(e) && t0 + cc / kPieces < ctx;
+                r[u] = nvr::load_stream(base + (cc / kPieces) * int(token_stride) + 8 * (cc % kPieces));
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < kVLoads; ++u) {
+                const int cc = int(threadIdx.x) + kThreads * u;
+                const int t = t0 + cc / kPieces;
+                const int ph = phys(min(t, ctx - 1));
+                ok[u] = t < ctx && ph >= 0;
+                r[u] = nvr::load_stream(vcol + int64_t(ok[u] ? ph : 0) * token_stride + 8 * (cc % kPieces));
+            }
         }
     };
     bool okW[kVLoads], okX[kVLoads], okY[kVLoads];
@@ -462,7 +492,10 @@ void launch_layout(nv_context* c, const uint16_t* q, const uint16_t* k, const ui
     const dim3 grid(unsigned(rows), unsigned(qh / HPB));
     const bool pow2 = (bs & (bs - 1)) == 0;
     const int shift = pow2 ? __builtin_ctz(unsigned(bs)) : 0;
-    if (pow2 && bs >= L::kStep && bs >= L::kVTile)
+    // kAligned also needs the row's table in one wave (at most 64 entries) and
+    // in-block offsets that fit in int32.
+    if (pow2 && bs >= L::kStep && bs >= L::kVTile && (max_context - 1) / bs < kWave &&
+        int64_t(bs) * kvh * DIM < (int64_t(1) << 31))
         hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAligned, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v,
                            p, s, t, o, qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride);
     else if (pow2)
