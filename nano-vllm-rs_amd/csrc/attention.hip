@@ -160,15 +160,16 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     // kAligned: the block entry of the aligned group (a K step or a V tile)
     // that starts at logical token t0 (clamped into the context; uniform),
     // whether it is a valid block, and the address of the group's first token
-    // row in `col` (block 0 for an invalid entry, so that every load of the
-    // group stays inside an allocated block; its data is then discarded).
+    // row in `col`. A group past the context or in an invalid block reads the
+    // first rows of physical block 0 instead: every load stays inside an
+    // allocated block, its data is discarded, and all such reads share the
+    // same lines (cache hits rather than HBM traffic).
     auto group_entry = [&](int t0) -> int {
         return __builtin_amdgcn_readlane(lane_entry, min(t0, ctx - 1) >> bs_shift);
     };
     auto entry_ok = [&](int e) { return e >= 0 && e < blocks; };
     auto group_base = [&](const uint16_t* col, int e, int t0) {
-        return col + (entry_ok(e) ? int64_t(e) * bs * token_stride : int64_t(0)) +
-               int64_t(t0 & (bs - 1)) * token_stride;
+        return t0 < ctx && entry_ok(e) ? col + (int64_t(e) * bs + (t0 & (bs - 1))) * token_stride : col;
     };
 
     // ---- 1. scores ----
