@@ -516,6 +516,17 @@ def test_attention_invalid_rows_and_blocks(gpu):
     assert not want[1].any() and not want[3].any() and not want[4].any()
 
 
+def test_attention_aligned_blocks_with_holes_mid_context(gpu):
+    """256-token blocks (whole K steps and V tiles per block: the block table is
+    read once per step from a register) with invalid entries in the middle and
+    at the end of long contexts, and contexts ending inside a step or a tile."""
+    batch, stride, bs = 4, 16, 256
+    pos = [999, 4095, 700, 63, 64, 1023, 2047, 300]
+    seqs = [0, 1, 2, 3, 0, 1, 2, 3]
+    holes = [(1, -1), (stride + 7, batch * stride + 5), (2 * stride + 2, -3), (3 * stride + 1, batch * stride)]
+    _attention_case(gpu, 235, pos, seqs, 16, 8, 128, bs, batch, stride, 4096, holes=holes)
+
+
 def test_attention_generic_path_for_unaligned_queries(gpu):
     _attention_case(gpu, 240, [0, 77, 399], [0, 1, 1], 4, 2, 128, 16, 2, 25, 400, align=False)
 
