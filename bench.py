@@ -508,10 +508,13 @@ def main() -> int:
                              "frac": round(gbs / HBM_PEAK_GBS, 4), "rows_per_s": round(rows / (t / 1e3), 1),
                              "launches": len(launches)}
 
-    # Dominant kernel of the step: largest launches x time at the step's shape.
+    # Dominant kernel of the step: the largest share of the step's HBM bytes
+    # (launches x algorithmic bytes at the step's shape). By time, SiLU and
+    # qkv_rope tie within run-to-run noise; by bytes SiLU leads (4.23 GB of
+    # 11.9 GB per step), so the choice is stable.
     roofline = None
     shape_of = {"add_rms": "add_rms_8192x1024", "qkv_rope_cached": "qkv_rope_8192", "silu": "silu_8192x6144"}
-    share = {k: chain.launches()[k] * kernels[v]["us"] for k, v in shape_of.items() if v in kernels}
+    share = {k: chain.launches()[k] * kernels[v]["bytes"] for k, v in shape_of.items() if v in kernels}
     if share:
         dom = max(share, key=share.get)
         kd = kernels[shape_of[dom]]
