@@ -389,6 +389,23 @@ def measured_traffic(case):
     return None
 
 
+SCLK_GHZ = 2.4  # MI355X peak engine clock
+
+
+def measured_valu(case):
+    """VALU wave-instructions per launch of a sampling case from the committed
+    rocprofv3 SQ_INSTS_VALU summary, or None when the summary does not list it."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "sampling_valu.txt")
+    try:
+        for line in open(path):
+            tok = line.split()
+            if len(tok) >= 9 and tok[0] == case and tok[1].isdigit():
+                return int(tok[1])
+    except OSError:
+        pass
+    return None
+
+
 def run_kernel_case(gpu, hip, launches, rounds):
     """Average launch time (ms) over `rounds` passes through the rotating sets."""
     graph = gpu.capture(lambda: [f() for f in launches])
@@ -507,6 +524,12 @@ def main() -> int:
             kernels[name] = {"workload": workload, "us": round(t * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
                              "frac": round(gbs / HBM_PEAK_GBS, 4), "rows_per_s": round(rows / (t / 1e3), 1),
                              "launches": len(launches)}
+            valu = measured_valu(name)
+            if valu is not None:
+                # VALU roofline: one wave64 VALU instruction per CU per cycle.
+                floor_us = valu / (gpu.sm_count() * SCLK_GHZ * 1e3)
+                kernels[name]["valu"] = {"insts": valu, "floor_us": round(floor_us, 2),
+                                         "frac": round(floor_us / (t * 1e3), 4)}
 
     # Dominant kernel of the step: the largest share of the step's HBM bytes
     # (launches x algorithmic bytes at the step's shape). By time, SiLU and

@@ -4,7 +4,9 @@
 // forward, then D decode steps of S rows at T = 0.6, each one HIP graph
 // replay. The eager forward of the same decode steps is timed too.
 //
-// Usage: decode_bench [S=8] [D=127]   -> one JSON line on stdout.
+// Usage: decode_bench [S=8] [D=127] [eager]   -> one JSON line on stdout.
+// With "eager" no graph is captured (both timed loops launch eagerly), for
+// profilers that do not follow graph launches.
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -64,6 +66,7 @@ int main(int argc, char** argv) {
     const std::size_t D = argc > 2 ? std::strtoul(argv[2], nullptr, 10) : 127;
     nvr::ModelConfig config;     // Qwen3-0.6B
     nvr::ModelOptions options;   // block 256, 128 blocks, 1024 batch tokens, 32 sequences, 4096 context
+    options.graphs = !(argc > 3 && std::strcmp(argv[3], "eager") == 0);
     if (S == 0 || S > options.max_sequences || 1024 % S != 0) {
         std::fprintf(stderr, "S must divide 1024 and be at most %zu\n", options.max_sequences);
         return 2;
