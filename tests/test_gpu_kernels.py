@@ -494,7 +494,8 @@ def test_attention_many_rows_odd_block_size(gpu):
 
 
 @pytest.mark.parametrize("dim,qh,kvh,bs", [(32, 4, 2, 8), (64, 8, 2, 256), (256, 4, 4, 16), (128, 6, 2, 7),
-                                           (128, 4, 4, 32), (80, 4, 2, 16), (96, 2, 1, 5), (2, 2, 2, 4)])
+                                           (128, 4, 4, 32), (80, 4, 2, 16), (96, 2, 1, 5), (2, 2, 2, 4),
+                                           (32, 4, 2, 256), (128, 8, 8, 64), (64, 2, 2, 128)])
 def test_attention_head_dims_groups_and_block_sizes(gpu, dim, qh, kvh, bs):
     rng = np.random.default_rng(dim * 7 + bs)
     batch, max_context = 4, 520
