@@ -349,6 +349,30 @@ def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain, only=()):
                                                        ablocks, astride, ab, actx) for i in range(4)],
                       bytes_attention(ab, actx, astride), ab))
 
+    # Paged attention, small decode batch: 8 sequences at context 1024 (one
+    # query row each), the serving shape where each block walks its context
+    # alone on a CU. The caches (8 x 4 blocks of 256 tokens) rotate over sets
+    # that together exceed the MALL.
+    if want("attention_decode_8x1024"):
+        db, dctx = 8, 1024
+        dstride = MAX_POS // BS
+        dper = dctx // BS
+        dsets = sets_for(2 * db * dper * BS * KVH * D * 2)
+        dkc = [fill.normal(db * dper * BS * KVH * D * 2) for _ in range(dsets)]
+        dvc = [fill.normal(db * dper * BS * KVH * D * 2) for _ in range(dsets)]
+        dtab = np.full((db, dstride), -1, np.int32)
+        dtab[:, :dper] = np.random.default_rng(12).permutation(db * dper).reshape(db, dper)
+        dtab = fill.ints(dtab.reshape(-1))
+        dpos = fill.ints(np.full(db, dctx - 1, np.int32))
+        dseq = fill.ints(np.arange(db, dtype=np.int32))
+        dq = fill.normal(db * QH * D * 2)
+        dout = gpu.alloc(db * QH * D * 2)
+        cases.append(("attention_decode_8x1024", "paged GQA attention, 8 decode rows x 1024 context, 16/8 heads, "
+                      "dim 128, 256-token blocks",
+                      [lambda i=i: gpu.paged_attention(dq, dkc[i], dvc[i], dpos, dseq, dtab, dout, db, QH, KVH, D, BS,
+                                                       db * dper, dstride, db, MAX_POS) for i in range(dsets)],
+                      bytes_attention(db, dctx, dstride), db))
+
     # Sampling 256 x 151936: rows 0-127 greedy, 128-255 Gumbel at T=0.6.
     if not want("sampling_256x151936", "sampling_greedy", "sampling_gumbel"):
         return cases
