@@ -94,7 +94,9 @@ struct OrderedLayout {
     static constexpr int kStep = kQuads * kW;             // tokens per block step
     static constexpr int kKLoads = kQuads / kRowsPerLoad; // load instructions per wave step (= P)
     static constexpr int kKRow = DIM * 2 + 64;            // staged K row bytes; the pad makes quad reads conflict-free
-    static constexpr int kVTile = (OCC ? 4096 : 8192) / DIM;  // tokens per V tile (8 or 16 KB)
+    // Tokens per V tile: 8 KB (OCC), 16 KB, or 32 KB with 512 threads (at
+    // most one block per two CUs, so LDS is not the limit).
+    static constexpr int kVTile = (OCC ? 4096 : TPB > kThreads ? 16384 : 8192) / DIM;
     static constexpr int kVLoads = kVTile * kPieces / TPB;  // V loads per thread per tile (1 to 4)
     static constexpr int kKStage = kW * kQuads * kKRow;
     static constexpr int kVStage = 2 * kVTile * DIM * 2;
