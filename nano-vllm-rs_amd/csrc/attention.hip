@@ -80,28 +80,23 @@ __device__ __forceinline__ int64_t phys_token(int entry, int t, int bs, int bloc
 
 // Compile-time geometry of attention_ordered. OCC trades pipeline depth for
 // occupancy (see launch_ordered): 32-token V tiles instead of 64 and three K
-// buffers instead of four. TPB threads per block: 256, or 512 when a launch
-// has at most one block per CU (twice the waves for the scores).
-template <int DIM, int HPB, bool OCC, int TPB = kThreads>
+// buffers instead of four.
+template <int DIM, int HPB, bool OCC>
 struct OrderedLayout {
     static_assert(DIM % 32 == 0 && DIM <= 256 && HPB * DIM <= kThreads, "shape");
-    static_assert(TPB % kThreads == 0, "the denominator runs on the first 256 threads");
-    static constexpr int kW = TPB / kWave;                // waves per block
     static constexpr int P = DIM / 32;                    // elements per dot chain
     static constexpr int kPieces = DIM / 8;               // 16-byte pieces per K/V row
     static constexpr int kRowsPerLoad = kWave / kPieces;  // whole rows per wave load instruction
     static constexpr int kQuads = kWave / 4;              // tokens per wave per phase-1 step
-    static constexpr int kStep = kQuads * kW;             // tokens per block step
+    static constexpr int kStep = kQuads * kWaves;         // tokens per block step
     static constexpr int kKLoads = kQuads / kRowsPerLoad; // load instructions per wave step (= P)
     static constexpr int kKRow = DIM * 2 + 64;            // staged K row bytes; the pad makes quad reads conflict-free
-    // Tokens per V tile: 8 KB (OCC), 16 KB, or 32 KB with 512 threads (at
-    // most one block per two CUs, so LDS is not the limit).
-    static constexpr int kVTile = (OCC ? 4096 : TPB > kThreads ? 16384 : 8192) / DIM;
-    static constexpr int kVLoads = kVTile * kPieces / TPB;  // V loads per thread per tile (1 to 4)
-    static constexpr int kKStage = kW * kQuads * kKRow;
+    static constexpr int kVTile = (OCC ? 4096 : 8192) / DIM;  // tokens per V tile (8 or 16 KB)
+    static constexpr int kVLoads = kVTile * kPieces / kThreads;  // V loads per thread per tile (2 or 4)
+    static constexpr int kKStage = kWaves * kQuads * kKRow;
     static constexpr int kVStage = 2 * kVTile * DIM * 2;
     static constexpr int kStageBytes = kKStage > kVStage ? kKStage : kVStage;
-    static_assert(kKLoads * kRowsPerLoad == kQuads && kVLoads * TPB == kVTile * kPieces, "tiles");
+    static_assert(kKLoads * kRowsPerLoad == kQuads && kVLoads * kThreads == kVTile * kPieces, "tiles");
 };
 
 // How a logical token finds its physical row: kAnyBs divides by the block
@@ -109,14 +104,13 @@ struct OrderedLayout {
 // whole K steps and V tiles) looks the block entry up once per step or tile.
 constexpr int kAnyBs = 0, kPow2 = 1, kAligned = 2;
 
-template <int DIM, int HPB, int TABLE, bool OCC, int TPB>
-__global__ __launch_bounds__(TPB) void attention_ordered(
+template <int DIM, int HPB, int TABLE, bool OCC>
+__global__ __launch_bounds__(kThreads) void attention_ordered(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const int* __restrict__ positions, const int* __restrict__ seqs, const int* __restrict__ tables,
     uint16_t* __restrict__ out, int qh, int kvh, int bs, int bs_shift, int blocks, int stride, int batch,
     int max_context, int score_stride) {
-    using L = OrderedLayout<DIM, HPB, OCC, TPB>;
-    constexpr int kW = L::kW;
+    using L = OrderedLayout<DIM, HPB, OCC>;
     constexpr int P = L::P, kPieces = L::kPieces, kQuads = L::kQuads, kStep = L::kStep;
     constexpr int kRowsPerLoad = L::kRowsPerLoad, kKLoads = L::kKLoads, kKRow = L::kKRow;
     constexpr int kVTile = L::kVTile, kVLoads = L::kVLoads;
@@ -125,8 +119,8 @@ __global__ __launch_bounds__(TPB) void attention_ordered(
     float* probs = reinterpret_cast<float*>(smem);                          // [HPB][score_stride]
     unsigned char* stage = smem + sizeof(float) * HPB * score_stride;       // K rows (phase 1) / V slots (phase 3)
     int* ltable = reinterpret_cast<int*>(stage + L::kStageBytes);           // the row's block-table entries
-    __shared__ float red_max[HPB][kW];
-    __shared__ float red_sum[HPB][2 * kWaves];  // the reference's 8 warps of 32
+    __shared__ float red_max[HPB][kWaves];
+    __shared__ float red_sum[HPB][2 * kWaves];
 
     const int row = blockIdx.x;
     const int h0 = blockIdx.y * HPB;
@@ -136,7 +130,7 @@ __global__ __launch_bounds__(TPB) void attention_ordered(
     uint16_t* orow = out + (int64_t(row) * qh + h0) * DIM;
     if (seq < 0 || seq >= batch || context64 < 1 || context64 > max_context ||
         context64 > int64_t(stride) * bs) {
-        for (int i = threadIdx.x; i < HPB * DIM; i += TPB) orow[i] = 0;
+        for (int i = threadIdx.x; i < HPB * DIM; i += kThreads) orow[i] = 0;
         return;
     }
     const int ctx = int(context64);
@@ -151,7 +145,7 @@ __global__ __launch_bounds__(TPB) void attention_ordered(
     if constexpr (TABLE == kAligned) {
         if (lane < nent) lane_entry = table[lane];
     } else {
-        for (int i = threadIdx.x; i < nent; i += TPB) ltable[i] = table[i];
+        for (int i = threadIdx.x; i < nent; i += kThreads) ltable[i] = table[i];
         __syncthreads();
     }
     // Physical token row (block * bs + offset) of logical token t < ctx, or -1
@@ -306,14 +300,14 @@ __global__ __launch_bounds__(TPB) void attention_ordered(
             const uint16_t* base = group_base(vcol, e, t0);
 #pragma unroll
             for (int u = 0; u < kVLoads; ++u) {
-                const int cc = int(threadIdx.x) + TPB * u;
+                const int cc = int(threadIdx.x) + kThreads * u;
                 ok[u] = entry_ok(e) && t0 + cc / kPieces < ctx;
                 r[u] = nvr::load_stream(base + (cc / kPieces) * int(token_stride) + 8 * (cc % kPieces));
             }
         } else {
 #pragma unroll
             for (int u = 0; u < kVLoads; ++u) {
-                const int cc = int(threadIdx.x) + TPB * u;
+                const int cc = int(threadIdx.x) + kThreads * u;
                 const int t = t0 + cc / kPieces;
                 const int ph = phys(min(t, ctx - 1));
                 ok[u] = t < ctx && ph >= 0;
@@ -337,22 +331,16 @@ __global__ __launch_bounds__(TPB) void attention_ordered(
     float den[HPB];
 #pragma unroll
     for (int g = 0; g < HPB; ++g) {
-        float mg = red_max[g][0];
-#pragma unroll
-        for (int w = 1; w < kW; ++w) mg = fmaxf(mg, red_max[g][w]);
+        const float mg = fmaxf(fmaxf(red_max[g][0], red_max[g][1]), fmaxf(red_max[g][2], red_max[g][3]));
         const bool finite = __builtin_isfinite(mg);
-        // The first 256 threads (waves 0-3, whole) do the exps and the
-        // reference's block sum: thread i sums p_i, p_{i+256}, ... in order.
-        if (threadIdx.x < kThreads) {
-            float sum = 0.0f;
-            for (int t = threadIdx.x; t < ctx; t += kThreads) {
-                const float pr = finite ? nvr::nvr_expf(probs[g * score_stride + t] - mg) : 0.0f;
-                probs[g * score_stride + t] = pr;
-                sum += pr;
-            }
-            sum = half_wave_sum(sum);
-            if ((lane & 31) == 0) red_sum[g][2 * wave + (lane >> 5)] = sum;
+        float sum = 0.0f;
+        for (int t = threadIdx.x; t < ctx; t += kThreads) {
+            const float pr = finite ? nvr::nvr_expf(probs[g * score_stride + t] - mg) : 0.0f;
+            probs[g * score_stride + t] = pr;
+            sum += pr;
         }
+        sum = half_wave_sum(sum);
+        if ((lane & 31) == 0) red_sum[g][2 * wave + (lane >> 5)] = sum;
     }
     __syncthreads();
 #pragma unroll
@@ -370,7 +358,7 @@ __global__ __launch_bounds__(TPB) void attention_ordered(
     auto put = [&](const uint4 (&r)[kVLoads], const bool (&ok)[kVLoads], int slot) {
 #pragma unroll
         for (int u = 0; u < kVLoads; ++u)
-            *reinterpret_cast<uint4*>(slots + slot * kVTile * DIM + 8 * (int(threadIdx.x) + TPB * u)) =
+            *reinterpret_cast<uint4*>(slots + slot * kVTile * DIM + 8 * (int(threadIdx.x) + kThreads * u)) =
                 ok[u] ? r[u] : make_uint4(kNegZeroPair, kNegZeroPair, kNegZeroPair, kNegZeroPair);
         __syncthreads();
     };
@@ -493,14 +481,15 @@ __global__ __launch_bounds__(kThreads) void attention_direct(
     }
 }
 
-template <int DIM, int HPB, bool OCC, int TPB = kThreads>
+template <int DIM, int HPB, bool OCC>
 void launch_layout(nv_context* c, const uint16_t* q, const uint16_t* k, const uint16_t* v, const int* p, const int* s,
                    const int* t, uint16_t* o, int rows, int qh, int kvh, int bs, int blocks, int stride, int batch,
                    int max_context) {
     const int score_stride = (max_context + 3) & ~3;
     const int table_entries = (max_context - 1) / bs + 1;
-    using L = OrderedLayout<DIM, HPB, OCC, TPB>;
-    const size_t lds = sizeof(float) * HPB * score_stride + L::kStageBytes + sizeof(int) * table_entries;
+    const size_t lds = sizeof(float) * HPB * score_stride + OrderedLayout<DIM, HPB, OCC>::kStageBytes +
+                       sizeof(int) * table_entries;
+    using L = OrderedLayout<DIM, HPB, OCC>;
     const dim3 grid(unsigned(rows), unsigned(qh / HPB));
     const bool pow2 = (bs & (bs - 1)) == 0;
     const int shift = pow2 ? __builtin_ctz(unsigned(bs)) : 0;
@@ -508,13 +497,13 @@ void launch_layout(nv_context* c, const uint16_t* q, const uint16_t* k, const ui
     // in-block offsets that fit in int32.
     if (pow2 && bs >= L::kStep && bs >= L::kVTile && (max_context - 1) / bs < kWave &&
         int64_t(bs) * kvh * DIM < (int64_t(1) << 31))
-        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAligned, OCC, TPB>), grid, dim3(TPB), lds, c->stream, q, k, v,
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAligned, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v,
                            p, s, t, o, qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride);
     else if (pow2)
-        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kPow2, OCC, TPB>), grid, dim3(TPB), lds, c->stream, q, k, v, p,
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kPow2, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v, p,
                            s, t, o, qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride);
     else
-        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAnyBs, OCC, TPB>), grid, dim3(TPB), lds, c->stream, q, k, v,
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAnyBs, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v,
                            p, s, t, o, qh, kvh, bs, 0, blocks, stride, batch, max_context, score_stride);
 }
 
@@ -533,18 +522,6 @@ void launch_ordered(nv_context* c, const uint16_t* q, const uint16_t* k, const u
         if (groups > 2 * int64_t(c->cu_count > 0 ? c->cu_count : 256)) {
             launch_layout<DIM, HPB, true>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride, batch,
                                           max_context);
-            return;
-        }
-    }
-    if constexpr (DIM <= 128) {
-        // At most one block per two CUs: nothing else on a CU hides a
-        // block's latencies, so the block takes 512 threads (twice the score
-        // waves). Measured on MI355X: 8 rows x 1024 tokens 30.5 -> 27.5 us,
-        // 1 row 30.2 -> 25.5 us, 8 x 130 9.0 vs 9.1 us; at one block per CU
-        // (32 rows x 8 pairs) short contexts lost (11.1 -> 12.7 us at 130).
-        if (2 * int64_t(rows) * (qh / HPB) <= int64_t(c->cu_count > 0 ? c->cu_count : 256)) {
-            launch_layout<DIM, HPB, false, 2 * kThreads>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride,
-                                                         batch, max_context);
             return;
         }
     }
