@@ -124,6 +124,18 @@ int nv_attention(nv_context* c, const void* q, const void* kc, const void* vc,
                  int rows, int qh, int kvh, int dim, int bs, int blocks, int stride, int batch,
                  int max_context);
 
+/* No single counterpart in the reference: nv_qkv_rope_cached followed by
+ * nv_attention (kernels/kernels.cu:166-211,474 then 475-485) in one launch for
+ * decode batches, with the same outputs (out; K and V at slots[r]) bit for bit
+ * and without writing the rotated q to memory. Head dim 128 and 16-byte
+ * aligned tensors only (else -2). No row may read a KV slot that another row
+ * of the call writes: rows do not wait for each other's cache writes. */
+int nv_attention_qkv_rope(nv_context* c, const void* qkv, const void* qw, const void* kw,
+                          const void* positions, const void* slots, void* kc, void* vc,
+                          const void* seqs, const void* tables, void* out, int rows, int qh, int kvh,
+                          int dim, int bs, int blocks, int stride, int batch, int max_context, float eps,
+                          const void* rope_cache, int max_positions);
+
 /* kernels/kernels.cu:356-365,486 — out[r,i] = bf16(silu(gate) * up) with
  * packed = [rows, 2, intermediate] (src/gpu.rs:996-1019). */
 int nv_silu(nv_context* c, const void* packed, void* out, int rows, int intermediate);

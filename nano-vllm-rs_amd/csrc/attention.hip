@@ -104,12 +104,24 @@ struct OrderedLayout {
 // whole K steps and V tiles) looks the block entry up once per step or tile.
 constexpr int kAnyBs = 0, kPow2 = 1, kAligned = 2;
 
-template <int DIM, int HPB, int TABLE, bool OCC>
+// The q/k norm + RoPE + KV-slot write that FUSED blocks run first (the
+// decode-batch entry point); unused otherwise.
+struct QkvRopeArgs {
+    const uint16_t* qkv;   // [rows, qh + 2 kvh, 128]
+    const uint16_t* qw;    // q norm weight [128]
+    const uint16_t* kw;    // k norm weight [128]
+    const int* slots;      // [rows]
+    const float* rope;     // [max_positions, 128]: cos | sin
+    int max_positions;
+    float eps;
+};
+
+template <int DIM, int HPB, int TABLE, bool OCC, bool FUSED>
 __global__ __launch_bounds__(kThreads) void attention_ordered(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    const uint16_t* __restrict__ q, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
     const int* __restrict__ positions, const int* __restrict__ seqs, const int* __restrict__ tables,
     uint16_t* __restrict__ out, int qh, int kvh, int bs, int bs_shift, int blocks, int stride, int batch,
-    int max_context, int score_stride) {
+    int max_context, int score_stride, QkvRopeArgs fa) {
     using L = OrderedLayout<DIM, HPB, OCC>;
     constexpr int P = L::P, kPieces = L::kPieces, kQuads = L::kQuads, kStep = L::kStep;
     constexpr int kRowsPerLoad = L::kRowsPerLoad, kKLoads = L::kKLoads, kKRow = L::kKRow;
@@ -128,6 +140,56 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     const int seq = seqs[row];
     const int64_t context64 = int64_t(positions[row]) + 1;
     uint16_t* orow = out + (int64_t(row) * qh + h0) * DIM;
+
+    // ---- 0. (FUSED) this row's q/k norm + RoPE and its KV-slot write ----
+    // Wave 0, one 16-lane group per head in the layout of qkv_rope's d128
+    // kernel (lane m holds elements 8m..8m+7) and the same arithmetic
+    // (nvr::norm_rotate_d128): groups g < HPB normalise and rotate q head
+    // h0 + g into LDS; group HPB does the kv head's K and writes it to the
+    // cache slot; group HPB + 1 copies its V. With one q head per block the
+    // two blocks of a kv head write the same bytes. The barrier orders those
+    // stores before this block's K/V loads. It runs for every row, as the
+    // separate q/k-norm + RoPE launch would, also those the attention below
+    // then skips.
+    __shared__ __align__(16) uint16_t qs[FUSED ? HPB : 1][FUSED ? DIM : 8];
+    if constexpr (FUSED) {
+        static_assert(DIM == 128, "the fused q/k norm + RoPE runs at head dim 128");
+        if (threadIdx.x < kWave) {
+            const int grp = (threadIdx.x >> 4) & 3, m = threadIdx.x & 15;
+            const int heads = qh + 2 * kvh;
+            const bool qgrp = grp < HPB, kgrp = grp == HPB, vgrp = grp == HPB + 1;
+            const int hsel = qgrp ? h0 + grp : kgrp ? qh + kvhead : qh + kvh + kvhead;  // idle group: a v head
+            const uint4 xw = nvr::load_stream(fa.qkv + (int64_t(row) * heads + hsel) * DIM + 8 * m);
+            const uint4 wv = *reinterpret_cast<const uint4*>((qgrp ? fa.qw : fa.kw) + 8 * m);
+            const int pos = positions[row];
+            const int slot = fa.slots[row];
+            const bool valid_slot = slot >= 0 && int64_t(slot) < int64_t(bs) * blocks;
+            const int pair0 = 8 * (m & 7);
+            float cs[8], sn[8], wf[8];
+            if (pos >= 0 && pos < fa.max_positions) {
+                const float4* t = reinterpret_cast<const float4*>(fa.rope + int64_t(pos) * DIM + pair0);
+                const float4 c0 = t[0], c1 = t[1], s0 = t[DIM / 8], s1 = t[DIM / 8 + 1];
+                cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w;
+                cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
+                sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w;
+                sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) { cs[i] = 1.0f; sn[i] = 0.0f; }
+            }
+            if (m < 8) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) sn[i] = -sn[i];
+            }
+            nvr::unpack8(wv, wf);
+            const uint4 rot = nvr::norm_rotate_d128(xw, wf, cs, sn, fa.eps);
+            if (qgrp) *reinterpret_cast<uint4*>(&qs[qgrp ? grp : 0][8 * m]) = rot;
+            if (kgrp & valid_slot) nvr::store_stream(kc + (int64_t(slot) * kvh + kvhead) * DIM + 8 * m, rot);
+            if (vgrp & valid_slot) nvr::store_stream(vc + (int64_t(slot) * kvh + kvhead) * DIM + 8 * m, xw);
+        }
+        __syncthreads();
+    }
+
     if (seq < 0 || seq >= batch || context64 < 1 || context64 > max_context ||
         context64 > int64_t(stride) * bs) {
         for (int i = threadIdx.x; i < HPB * DIM; i += kThreads) orow[i] = 0;
@@ -188,7 +250,8 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     for (int g = 0; g < HPB; ++g)
 #pragma unroll
         for (int j = 0; j < P; ++j)
-            nvr::unpack8(*reinterpret_cast<const uint4*>(q + (int64_t(row) * qh + h0 + g) * DIM + 32 * j + 8 * a),
+            nvr::unpack8(FUSED ? *reinterpret_cast<const uint4*>(&qs[FUSED ? g : 0][FUSED ? 32 * j + 8 * a : 0])
+                               : *reinterpret_cast<const uint4*>(q + (int64_t(row) * qh + h0 + g) * DIM + 32 * j + 8 * a),
                          qf[g][j]);
     const float kScale = 1.0f / sqrtf(float(DIM));
     float m[HPB];
@@ -481,15 +544,16 @@ __global__ __launch_bounds__(kThreads) void attention_direct(
     }
 }
 
-template <int DIM, int HPB, bool OCC>
-void launch_layout(nv_context* c, const uint16_t* q, const uint16_t* k, const uint16_t* v, const int* p, const int* s,
+// Launch geometry of the ordered kernels. FUSED launches (head dim 128 only)
+// also run the rows' q/k norm + RoPE + KV-slot write (QkvRopeArgs).
+template <int DIM, int HPB, bool OCC, bool FUSED>
+void launch_layout(nv_context* c, const uint16_t* q, uint16_t* k, uint16_t* v, const int* p, const int* s,
                    const int* t, uint16_t* o, int rows, int qh, int kvh, int bs, int blocks, int stride, int batch,
-                   int max_context) {
+                   int max_context, const QkvRopeArgs& fa) {
     const int score_stride = (max_context + 3) & ~3;
     const int table_entries = (max_context - 1) / bs + 1;
-    const size_t lds = sizeof(float) * HPB * score_stride + OrderedLayout<DIM, HPB, OCC>::kStageBytes +
-                       sizeof(int) * table_entries;
     using L = OrderedLayout<DIM, HPB, OCC>;
+    const size_t lds = sizeof(float) * HPB * score_stride + L::kStageBytes + sizeof(int) * table_entries;
     const dim3 grid(unsigned(rows), unsigned(qh / HPB));
     const bool pow2 = (bs & (bs - 1)) == 0;
     const int shift = pow2 ? __builtin_ctz(unsigned(bs)) : 0;
@@ -497,14 +561,17 @@ void launch_layout(nv_context* c, const uint16_t* q, const uint16_t* k, const ui
     // in-block offsets that fit in int32.
     if (pow2 && bs >= L::kStep && bs >= L::kVTile && (max_context - 1) / bs < kWave &&
         int64_t(bs) * kvh * DIM < (int64_t(1) << 31))
-        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAligned, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v,
-                           p, s, t, o, qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride);
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAligned, OCC, FUSED>), grid, dim3(kThreads), lds, c->stream,
+                           q, k, v, p, s, t, o, qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride,
+                           fa);
     else if (pow2)
-        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kPow2, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v, p,
-                           s, t, o, qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride);
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kPow2, OCC, FUSED>), grid, dim3(kThreads), lds, c->stream,
+                           q, k, v, p, s, t, o, qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride,
+                           fa);
     else
-        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAnyBs, OCC>), grid, dim3(kThreads), lds, c->stream, q, k, v,
-                           p, s, t, o, qh, kvh, bs, 0, blocks, stride, batch, max_context, score_stride);
+        hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAnyBs, OCC, FUSED>), grid, dim3(kThreads), lds, c->stream,
+                           q, k, v, p, s, t, o, qh, kvh, bs, 0, blocks, stride, batch, max_context, score_stride,
+                           fa);
 }
 
 // Blocks are (row, head group) and each walks its context serially, so when
@@ -512,36 +579,50 @@ void launch_layout(nv_context* c, const uint16_t* q, const uint16_t* k, const ui
 // blocks per CU at 164 VGPRs and 52 KB of LDS for head dim 128 and 4096
 // positions): measured on MI355X, 1024 prefill rows 164 -> 108 us (8 x 128
 // tokens) and 457 -> 348 us (one 1024-token prompt). With at most two per CU
-// the deeper pipelines win (64 x 4096 decode: 200 vs 210 us).
-template <int DIM, int HPB>
-void launch_ordered(nv_context* c, const uint16_t* q, const uint16_t* k, const uint16_t* v, const int* p,
+// the deeper pipelines win (64 x 4096 decode: 200 vs 210 us). FUSED launches
+// (decode batches) keep the default layout.
+template <int DIM, int HPB, bool FUSED = false>
+void launch_ordered(nv_context* c, const uint16_t* q, uint16_t* k, uint16_t* v, const int* p,
                     const int* s, const int* t, uint16_t* o, int rows, int qh, int kvh, int bs, int blocks,
-                    int stride, int batch, int max_context) {
-    if constexpr (DIM == 128 && HPB == 2) {
+                    int stride, int batch, int max_context, const QkvRopeArgs& fa = {}) {
+    if constexpr (DIM == 128 && HPB == 2 && !FUSED) {
         const int64_t groups = int64_t(rows) * (qh / HPB);
         if (groups > 2 * int64_t(c->cu_count > 0 ? c->cu_count : 256)) {
-            launch_layout<DIM, HPB, true>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride, batch,
-                                          max_context);
+            launch_layout<DIM, HPB, true, false>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride, batch,
+                                                 max_context, fa);
             return;
         }
     }
-    launch_layout<DIM, HPB, false>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride, batch, max_context);
+    launch_layout<DIM, HPB, false, FUSED>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride, batch,
+                                          max_context, fa);
 }
 
-template <int DIM>
-void launch_dim(nv_context* c, const uint16_t* q, const uint16_t* k, const uint16_t* v, const int* p, const int* s,
+template <int DIM, bool FUSED = false>
+void launch_dim(nv_context* c, const uint16_t* q, uint16_t* k, uint16_t* v, const int* p, const int* s,
                 const int* t, uint16_t* o, int rows, int qh, int kvh, int bs, int blocks, int stride, int batch,
-                int max_context) {
+                int max_context, const QkvRopeArgs& fa = {}) {
     // A GQA pair per block reads each K/V row once for two heads. With fewer
     // pairs than CUs (small decode batches) one head per block wins instead:
     // twice the blocks on an otherwise idle GPU (measured on MI355X at 8 rows:
     // 9.0 vs 10.4 us at 130 tokens of context, 30.5 vs 35.2 us at 1024).
     const int64_t cus = c->cu_count > 0 ? c->cu_count : 256;
     if (DIM <= 128 && (qh / kvh) % 2 == 0 && int64_t(rows) * (qh / 2) >= cus)
-        launch_ordered<DIM, (DIM <= 128 ? 2 : 1)>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride, batch,
-                                                  max_context);
+        launch_ordered<DIM, (DIM <= 128 ? 2 : 1), FUSED>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride,
+                                                         batch, max_context, fa);
     else
-        launch_ordered<DIM, 1>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride, batch, max_context);
+        launch_ordered<DIM, 1, FUSED>(c, q, k, v, p, s, t, o, rows, qh, kvh, bs, blocks, stride, batch, max_context,
+                                      fa);
+}
+
+int check_attention(int rows, int qh, int kvh, int dim, int bs, int blocks, int stride, int batch,
+                    int max_context) {
+    if (rows <= 0 || qh <= 0 || kvh <= 0 || dim <= 0 || bs <= 0 || blocks <= 0 || stride <= 0 || batch <= 0 ||
+        max_context <= 0)
+        return nvr::fail(-2, "attention: dimensions must be positive");
+    if (qh % kvh != 0 || dim % 2 != 0 || dim > 256 || qh > 65535)
+        return nvr::fail(-2, "attention: need qh %% kvh == 0, an even head dim <= 256 and qh <= 65535");
+    if (max_context > kMaxContext) return nvr::fail(-2, "attention: max_context above %d", kMaxContext);
+    return 0;
 }
 
 }  // namespace
@@ -550,15 +631,10 @@ extern "C" int nv_attention(nv_context* c, const void* q, const void* kc, const 
                             const void* seqs, const void* tables, void* out, int rows, int qh, int kvh, int dim,
                             int bs, int blocks, int stride, int batch, int max_context) {
     NVR_ACTIVATE(c);
-    if (rows <= 0 || qh <= 0 || kvh <= 0 || dim <= 0 || bs <= 0 || blocks <= 0 || stride <= 0 || batch <= 0 ||
-        max_context <= 0)
-        return nvr::fail(-2, "attention: dimensions must be positive");
-    if (qh % kvh != 0 || dim % 2 != 0 || dim > 256 || qh > 65535)
-        return nvr::fail(-2, "attention: need qh %% kvh == 0, an even head dim <= 256 and qh <= 65535");
-    if (max_context > kMaxContext) return nvr::fail(-2, "attention: max_context above %d", kMaxContext);
+    if (int e = check_attention(rows, qh, kvh, dim, bs, blocks, stride, batch, max_context)) return e;
     auto q16 = static_cast<const uint16_t*>(q);
-    auto k16 = static_cast<const uint16_t*>(kc);
-    auto v16 = static_cast<const uint16_t*>(vc);
+    auto k16 = static_cast<uint16_t*>(const_cast<void*>(kc));  // read only: this entry point writes no cache
+    auto v16 = static_cast<uint16_t*>(const_cast<void*>(vc));
     auto p32 = static_cast<const int*>(positions);
     auto s32 = static_cast<const int*>(seqs);
     auto t32 = static_cast<const int*>(tables);
@@ -579,5 +655,34 @@ extern "C" int nv_attention(nv_context* c, const void* q, const void* kc, const 
         hipLaunchKernelGGL(attention_direct, dim3(unsigned(rows), unsigned(qh)), dim3(kThreads),
                            sizeof(float) * size_t(max_context), c->stream, q16, k16, v16, p32, s32, t32, o16, qh,
                            kvh, dim, bs, blocks, stride, batch, max_context);
+    return nvr::launch_status();
+}
+
+// Decode form: nv_qkv_rope_cached's q/k norm + RoPE + KV-slot write run inside
+// the attention launch (QkvRopeArgs), so the rotated q never leaves LDS and
+// one launch per layer goes away. Each row's prologue finishes before that
+// row's blocks read the cache, but rows do not wait for each other: no row may
+// read a slot that another row of the call writes (one row per sequence, as in
+// a decode batch whose written slots sit in blocks no other row maps).
+extern "C" int nv_attention_qkv_rope(nv_context* c, const void* qkv, const void* qw, const void* kw,
+                                     const void* positions, const void* slots, void* kc, void* vc,
+                                     const void* seqs, const void* tables, void* out, int rows, int qh, int kvh,
+                                     int dim, int bs, int blocks, int stride, int batch, int max_context, float eps,
+                                     const void* rope_cache, int max_positions) {
+    NVR_ACTIVATE(c);
+    if (int e = check_attention(rows, qh, kvh, dim, bs, blocks, stride, batch, max_context)) return e;
+    if (dim != 128) return nvr::fail(-2, "attention_qkv_rope: head dim %d, the fused form needs 128", dim);
+    if (max_positions < 0) return nvr::fail(-2, "attention_qkv_rope: max_positions must be non-negative");
+    if (!(nvr::aligned(qkv, 16) && nvr::aligned(qw, 16) && nvr::aligned(kw, 16) && nvr::aligned(kc, 16) &&
+          nvr::aligned(vc, 16) && nvr::aligned(rope_cache, 16)) ||
+        int64_t(blocks) * bs > 0x7fffffff)
+        return nvr::fail(-2, "attention_qkv_rope: needs 16-byte aligned tensors and blocks * bs < 2^31");
+    const QkvRopeArgs fa{static_cast<const uint16_t*>(qkv), static_cast<const uint16_t*>(qw),
+                         static_cast<const uint16_t*>(kw), static_cast<const int*>(slots),
+                         static_cast<const float*>(rope_cache), max_positions, eps};
+    launch_dim<128, true>(c, nullptr, static_cast<uint16_t*>(kc), static_cast<uint16_t*>(vc),
+                          static_cast<const int*>(positions), static_cast<const int*>(seqs),
+                          static_cast<const int*>(tables), static_cast<uint16_t*>(out), rows, qh, kvh, bs, blocks,
+                          stride, batch, max_context, fa);
     return nvr::launch_status();
 }

@@ -245,4 +245,45 @@ __device__ __forceinline__ void rope_cos_sin(int position, int pair, int dim, fl
     *s = float(sd);
 }
 
+// q/k head: RMSNorm in the reference's order, bf16 rounding, NeoX rotation.
+// Returns the rotated chunk of this lane (elements 8m..8m+7), packed. The
+// 16 lanes of a head form one DPP row: warp level 16 is quad lane ^2, level 8
+// quad lane ^1; the warp sums (lanes 0,4,8,12) fold as (W0 + W2) + (W1 + W3)
+// through row_ror:8 then row_half_mirror (each quad holds one replicated sum).
+// sn_signed is -sin for elements j < 64 and +sin above, so that
+// rot = n*c + p*sn_signed rounds exactly like (n*c) -/+ (p*sin).
+__device__ __forceinline__ uint4 norm_rotate_d128(const uint4& xw, const float* wf, const float* cs,
+                                                  const float* sn_signed, float eps) {
+    constexpr int D = 128;
+    float x[8];
+    unpack8(xw, x);
+    float s[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = x[i] * x[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = s[i] + dpp<kDppQuadXor2>(s[i]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = s[i] + dpp<kDppQuadXor1>(s[i]);
+    float total = ((s[0] + s[4]) + (s[2] + s[6])) + ((s[1] + s[5]) + (s[3] + s[7]));
+    total = total + dpp<kDppRowRor8>(total);
+    total = total + dpp<kDppRowHalfMirror>(total);
+    const float inv = inv_sqrt_rn(total / float(D) + eps);
+    float n[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) n[i] = (x[i] * inv) * wf[i];
+    const uint4 np = pack8(n);  // the bf16-materialised normalised head
+    unpack8(np, n);
+    uint4 pp;  // NeoX partner chunk (elements j +/- 64) from lane m ^ 8
+    pp.x = dpp<kDppRowRor8>(np.x);
+    pp.y = dpp<kDppRowRor8>(np.y);
+    pp.z = dpp<kDppRowRor8>(np.z);
+    pp.w = dpp<kDppRowRor8>(np.w);
+    float p[8];
+    unpack8(pp, p);
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = n[i] * cs[i] + p[i] * sn_signed[i];
+    return pack8(o);
+}
+
 }  // namespace nvr

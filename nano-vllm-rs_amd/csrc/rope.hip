@@ -33,47 +33,6 @@ constexpr int kHeadLanes = 16;
 // Row count from which the d128 kernel uses four waves per row instead of two.
 constexpr int kRopeSplit4Rows = 4096;
 
-// q/k head: RMSNorm in the reference's order, bf16 rounding, NeoX rotation.
-// Returns the rotated chunk of this lane (elements 8m..8m+7), packed. The
-// 16 lanes of a head form one DPP row: warp level 16 is quad lane ^2, level 8
-// quad lane ^1; the warp sums (lanes 0,4,8,12) fold as (W0 + W2) + (W1 + W3)
-// through row_ror:8 then row_half_mirror (each quad holds one replicated sum).
-// sn_signed is -sin for elements j < 64 and +sin above, so that
-// rot = n*c + p*sn_signed rounds exactly like (n*c) -/+ (p*sin).
-__device__ __forceinline__ uint4 norm_rotate_d128(const uint4& xw, const float* wf, const float* cs,
-                                                  const float* sn_signed, float eps) {
-    constexpr int D = 128;
-    float x[8];
-    nvr::unpack8(xw, x);
-    float s[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s[i] = x[i] * x[i];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s[i] = s[i] + nvr::dpp<nvr::kDppQuadXor2>(s[i]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s[i] = s[i] + nvr::dpp<nvr::kDppQuadXor1>(s[i]);
-    float total = ((s[0] + s[4]) + (s[2] + s[6])) + ((s[1] + s[5]) + (s[3] + s[7]));
-    total = total + nvr::dpp<nvr::kDppRowRor8>(total);
-    total = total + nvr::dpp<nvr::kDppRowHalfMirror>(total);
-    const float inv = nvr::inv_sqrt_rn(total / float(D) + eps);
-    float n[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) n[i] = (x[i] * inv) * wf[i];
-    const uint4 np = nvr::pack8(n);  // the bf16-materialised normalised head
-    nvr::unpack8(np, n);
-    uint4 pp;  // NeoX partner chunk (elements j +/- 64) from lane m ^ 8
-    pp.x = nvr::dpp<nvr::kDppRowRor8>(np.x);
-    pp.y = nvr::dpp<nvr::kDppRowRor8>(np.y);
-    pp.z = nvr::dpp<nvr::kDppRowRor8>(np.z);
-    pp.w = nvr::dpp<nvr::kDppRowRor8>(np.w);
-    float p[8];
-    nvr::unpack8(pp, p);
-    float o[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = n[i] * cs[i] + p[i] * sn_signed[i];
-    return nvr::pack8(o);
-}
-
 // SPLIT waves per token row. The row's heads form quads 4Q..4Q+3; wave part
 // hw takes quads hw, hw+SPLIT, hw+2*SPLIT, ... and group g (16 lanes) of the
 // wave takes head 4Q + g of each of its quads. Lane m of a group holds
@@ -159,9 +118,9 @@ __global__ __launch_bounds__(256) void qkv_rope_d128(const uint16_t* __restrict_
                 if (valid_slot) nvr::store_stream(vc + (int64_t(slot) * kvh + (h - qh - kvh)) * D + 8 * m, xw[j]);
             } else if (h < qh) {
                 nvr::store_stream(qout + (int64_t(row) * qh + h) * D + 8 * m,
-                                  norm_rotate_d128(xw[j], qwf, cs, sn, eps));
+                                  nvr::norm_rotate_d128(xw[j], qwf, cs, sn, eps));
             } else {
-                const uint4 rot = norm_rotate_d128(xw[j], kwf, cs, sn, eps);
+                const uint4 rot = nvr::norm_rotate_d128(xw[j], kwf, cs, sn, eps);
                 if (valid_slot) nvr::store_stream(kc + (int64_t(slot) * kvh + (h - qh)) * D + 8 * m, rot);
             }
         }

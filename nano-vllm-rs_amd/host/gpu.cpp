@@ -348,6 +348,33 @@ void Gpu::paged_attention(const Buffer& q, const Buffer& kcache, const Buffer& v
                        dimension(batch_size), dimension(max_context)));
 }
 
+void Gpu::attention_qkv_rope(const Buffer& qkv, const Buffer& qweight, const Buffer& kweight,
+                             const Buffer& positions, const Buffer& slots, const Buffer& kcache,
+                             const Buffer& vcache, const Buffer& seq_indices, const Buffer& block_tables,
+                             const Buffer& out, std::size_t rows, std::size_t qheads, std::size_t kvheads,
+                             std::size_t head_dim, std::size_t block_size, std::size_t num_blocks,
+                             std::size_t table_stride, std::size_t batch_size, std::size_t max_context, float eps,
+                             const Buffer& rope_cache, std::size_t max_positions) const {
+    if (head_dim != 128) throw Error("fused attention needs head_dim 128");
+    if (max_context == 0 || max_context > 4096) throw Error("paged attention supports at most 4096 context tokens");
+    tensor(out, {rows, qheads, head_dim}, 2);
+    tensor(seq_indices, {rows}, 4);
+    tensor(block_tables, {batch_size, table_stride}, 4);
+    tensor(rope_cache, {max_positions, head_dim}, 4);
+    // The q/k norm + RoPE prologue reads and writes what qkv_rope_cached does
+    // (qout is not written: q stays on chip).
+    check_qkv_rope(qkv, qweight, kweight, positions, slots, out, kcache, vcache, rows, qheads, kvheads, head_dim,
+                   block_size, num_blocks, eps);
+    distinct(out, {&qkv, &kcache, &vcache, &positions, &seq_indices, &block_tables, &rope_cache});
+    for (const Buffer* cache : {&kcache, &vcache}) distinct(*cache, {&rope_cache, &seq_indices, &block_tables});
+    check(nv_attention_qkv_rope(handle(), qkv.ptr(), qweight.ptr(), kweight.ptr(), positions.ptr(), slots.ptr(),
+                                kcache.ptr(), vcache.ptr(), seq_indices.ptr(), block_tables.ptr(), out.ptr(),
+                                dimension(rows), dimension(qheads), dimension(kvheads), dimension(head_dim),
+                                dimension(block_size), dimension(num_blocks), dimension(table_stride),
+                                dimension(batch_size), dimension(max_context), eps, rope_cache.ptr(),
+                                dimension(max_positions)));
+}
+
 void Gpu::silu_mul(const Buffer& gateup, const Buffer& out, std::size_t rows, std::size_t intermediate) const {
     tensor(gateup, {rows, 2, intermediate}, 2);
     tensor(out, {rows, intermediate}, 2);

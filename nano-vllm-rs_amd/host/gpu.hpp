@@ -139,6 +139,16 @@ public:
                          std::size_t qheads, std::size_t kvheads, std::size_t head_dim, std::size_t block_size,
                          std::size_t num_blocks, std::size_t table_stride, std::size_t batch_size,
                          std::size_t max_context) const;
+    // Decode form of qkv_rope_cached followed by paged_attention (head dim 128):
+    // one launch, and the rotated q stays on chip. No row may read a KV slot
+    // that another row writes.
+    void attention_qkv_rope(const Buffer& qkv, const Buffer& qweight, const Buffer& kweight, const Buffer& positions,
+                            const Buffer& slots, const Buffer& kcache, const Buffer& vcache,
+                            const Buffer& seq_indices, const Buffer& block_tables, const Buffer& out,
+                            std::size_t rows, std::size_t qheads, std::size_t kvheads, std::size_t head_dim,
+                            std::size_t block_size, std::size_t num_blocks, std::size_t table_stride,
+                            std::size_t batch_size, std::size_t max_context, float eps, const Buffer& rope_cache,
+                            std::size_t max_positions) const;
     void silu_mul(const Buffer& gateup, const Buffer& out, std::size_t rows, std::size_t intermediate) const;
     void gather(const Buffer& x, const Buffer& indices, const Buffer& out, std::size_t rows, std::size_t hidden,
                 std::size_t input_rows) const;

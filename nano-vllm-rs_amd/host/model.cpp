@@ -197,7 +197,7 @@ QwenModel::QwenModel(const ModelConfig& config, const ModelOptions& options, con
 }
 
 // src/model.rs:635-818, without the FlashAttention branch.
-void QwenModel::forward(std::size_t rows, std::size_t sequences, std::size_t samples) const {
+void QwenModel::forward(std::size_t rows, std::size_t sequences, std::size_t samples, bool fused) const {
     const ModelConfig& c = config_;
     const ModelOptions& o = options_;
     const Workspace& w = work_;
@@ -212,12 +212,19 @@ void QwenModel::forward(std::size_t rows, std::size_t sequences, std::size_t sam
         else
             g.add_rms_norm(w.hidden, w.residual, l.input_norm, w.normed, rows, c.hidden_size, c.rms_norm_eps);
         g.gemm(w.normed, l.qkv, w.qkv, rows, qkv_size, c.hidden_size);
-        g.qkv_rope_cached(w.qkv, l.q_norm, l.k_norm, w.positions, w.slots, w.query, l.k_cache, l.v_cache, rows,
-                          c.num_attention_heads, c.num_key_value_heads, c.head_dim, o.block_size, o.num_blocks,
-                          c.rms_norm_eps, w.rope_cache, o.max_model_len);
-        g.paged_attention(w.query, l.k_cache, l.v_cache, w.positions, w.seq_indices, w.block_tables, w.attention, rows,
-                          c.num_attention_heads, c.num_key_value_heads, c.head_dim, o.block_size, o.num_blocks,
-                          table_stride_, sequences, o.max_model_len);
+        if (fused) {
+            g.attention_qkv_rope(w.qkv, l.q_norm, l.k_norm, w.positions, w.slots, l.k_cache, l.v_cache,
+                                 w.seq_indices, w.block_tables, w.attention, rows, c.num_attention_heads,
+                                 c.num_key_value_heads, c.head_dim, o.block_size, o.num_blocks, table_stride_,
+                                 sequences, o.max_model_len, c.rms_norm_eps, w.rope_cache, o.max_model_len);
+        } else {
+            g.qkv_rope_cached(w.qkv, l.q_norm, l.k_norm, w.positions, w.slots, w.query, l.k_cache, l.v_cache, rows,
+                              c.num_attention_heads, c.num_key_value_heads, c.head_dim, o.block_size, o.num_blocks,
+                              c.rms_norm_eps, w.rope_cache, o.max_model_len);
+            g.paged_attention(w.query, l.k_cache, l.v_cache, w.positions, w.seq_indices, w.block_tables, w.attention,
+                              rows, c.num_attention_heads, c.num_key_value_heads, c.head_dim, o.block_size,
+                              o.num_blocks, table_stride_, sequences, o.max_model_len);
+        }
         g.gemm(w.attention, l.attention_out, w.hidden, rows, c.hidden_size, q_size);
         g.add_rms_norm(w.hidden, w.residual, l.post_norm, w.normed, rows, c.hidden_size, c.rms_norm_eps);
         g.gemm(w.normed, l.gate_up, w.gate_up, rows, 2 * c.intermediate_size, c.hidden_size);
@@ -234,7 +241,7 @@ void QwenModel::forward(std::size_t rows, std::size_t sequences, std::size_t sam
 }
 
 // src/model.rs:820-923.
-std::array<std::size_t, 3> QwenModel::validate_batch(const Batch& b) const {
+std::array<std::size_t, 4> QwenModel::validate_batch(const Batch& b) const {
     const ModelOptions& o = options_;
     const std::size_t rows = b.token_ids.size(), samples = b.last_token_indices.size();
     ensure(rows > 0 && rows <= o.max_batch_tokens, "batch token count is outside model capacity");
@@ -274,30 +281,43 @@ std::array<std::size_t, 3> QwenModel::validate_batch(const Batch& b) const {
             ensure(block >= 0 && std::size_t(block) < o.num_blocks, "missing KV block in causal context");
         }
     }
-    return {rows, sequences, samples};
+    bool fused = config_.head_dim == 128 && rows == sequences;
+    std::map<int32_t, std::size_t> writer;  // block -> the row writing into it
+    for (std::size_t r = 0; fused && r < rows; ++r) {
+        fused = max_position[std::size_t(b.sequence_ids[r])] == b.positions[r];  // its sequence's only row
+        writer.emplace(int32_t(std::size_t(b.slot_mapping[r]) / o.block_size), r);
+    }
+    for (std::size_t r = 0; fused && r < rows; ++r) {
+        const int32_t* table = &b.block_tables[std::size_t(b.sequence_ids[r]) * b.table_stride];
+        for (std::size_t column = 0; fused && column <= std::size_t(b.positions[r]) / o.block_size; ++column) {
+            const auto it = writer.find(table[column]);
+            fused = it == writer.end() || it->second == r;
+        }
+    }
+    return {rows, sequences, samples, fused ? 1u : 0u};
 }
 
 // src/model.rs:925-987, without the FlashAttention metadata.
 std::vector<uint32_t> QwenModel::run(const Batch& batch) {
-    const auto [rows, sequences, samples] = validate_batch(batch);
+    const auto [rows, sequences, samples, fused] = validate_batch(batch);
     last_sample_count_ = 0;
     layout_.pack(host_metadata_, batch, sequences, table_stride_);
     // Upload synchronises before returning, so both eager launches and graph
     // replays see complete input and the staging vector may be reused.
     work_.metadata.upload_bytes(host_metadata_);
     if (options_.graphs && batch.is_decode && rows == sequences && samples == sequences) {
-        auto it = graphs_.find(rows);
+        auto it = graphs_.find(2 * rows + fused);
         if (it == graphs_.end()) {
             // hipBLAS may initialise state on first use of a shape: warm up
             // before capture; the replay then rewrites the same KV slots.
-            forward(rows, sequences, samples);
+            forward(rows, sequences, samples, fused);
             gpu_.sync();
-            Graph graph = gpu_.capture([&] { forward(rows, sequences, samples); });
-            it = graphs_.emplace(rows, std::move(graph)).first;
+            Graph graph = gpu_.capture([&] { forward(rows, sequences, samples, fused); });
+            it = graphs_.emplace(2 * rows + fused, std::move(graph)).first;
         }
         it->second.replay();
     } else {
-        forward(rows, sequences, samples);
+        forward(rows, sequences, samples, fused);
     }
     last_sample_count_ = samples;
     if (samples == 0) {

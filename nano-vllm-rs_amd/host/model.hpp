@@ -106,7 +106,10 @@ public:
     const Gpu& gpu() const { return gpu_; }
 
     // rows, sequences, samples of a valid batch (src/model.rs:820-923).
-    std::array<std::size_t, 3> validate_batch(const Batch& batch) const;
+    // {rows, sequences, samples, fused}: fused = 1 when the q/k norm + RoPE +
+    // KV write may run inside the attention launch (head dim 128, one row per
+    // sequence, and no row's context holds a block another row writes).
+    std::array<std::size_t, 4> validate_batch(const Batch& batch) const;
 
 private:
     struct Layer {
@@ -118,7 +121,7 @@ private:
         Buffer residual, hidden, normed, qkv, query, attention, gate_up, activated, gathered, logits;
     };
 
-    void forward(std::size_t rows, std::size_t sequences, std::size_t samples) const;
+    void forward(std::size_t rows, std::size_t sequences, std::size_t samples, bool fused) const;
 
     ModelConfig config_;
     ModelOptions options_;
@@ -130,7 +133,7 @@ private:
     Buffer embedding_, final_norm_, lm_head_;
     Workspace work_;
     ModelMemoryInfo memory_;
-    std::map<std::size_t, Graph> graphs_;  // decode row count -> captured forward
+    std::map<std::size_t, Graph> graphs_;  // 2 * decode row count + fused -> captured forward
     std::size_t last_sample_count_ = 0;
 };
 

@@ -57,6 +57,7 @@ SIGNATURES = {
     "nv_rope_cache": (_i, [_vp, _vp, _i, _i, _f]),
     "nv_qkv_rope_cached": (_i, [_vp] * 9 + [_i] * 6 + [_f, _vp, _i]),
     "nv_attention": (_i, [_vp] * 8 + [_i] * 9),
+    "nv_attention_qkv_rope": (_i, [_vp] * 11 + [_i] * 9 + [_f, _vp, _i]),
     "nv_silu": (_i, [_vp, _vp, _vp, _i, _i]),
     "nv_gather": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "nv_sample": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
@@ -460,6 +461,35 @@ class Gpu:
                                      _dimension(kvheads), _dimension(head_dim), _dimension(block_size),
                                      _dimension(num_blocks), _dimension(table_stride), _dimension(batch_size),
                                      _dimension(max_context)))
+
+    def attention_qkv_rope(self, qkv: Buffer, qweight: Buffer, kweight: Buffer, positions: Buffer, slots: Buffer,
+                           kcache: Buffer, vcache: Buffer, seq_indices: Buffer, block_tables: Buffer, out: Buffer,
+                           rows: int, qheads: int, kvheads: int, head_dim: int, block_size: int, num_blocks: int,
+                           table_stride: int, batch_size: int, max_context: int, eps: float, rope_cache: Buffer,
+                           max_positions: int) -> None:
+        """qkv_rope_cached followed by paged_attention in one launch (head dim
+        128), for decode batches: no row may read a KV slot that another row
+        writes. The rotated q is not written to memory."""
+        if head_dim != 128:
+            raise ValueError("fused attention needs head_dim 128")
+        if not 0 < max_context <= 4096:
+            raise ValueError("paged attention supports at most 4096 context tokens")
+        self.tensor(out, [rows, qheads, head_dim], 2)
+        self.tensor(seq_indices, [rows], 4)
+        self.tensor(block_tables, [batch_size, table_stride], 4)
+        self.tensor(rope_cache, [max_positions, head_dim], 4)
+        self._check_qkv_rope(qkv, qweight, kweight, positions, slots, out, kcache, vcache, rows, qheads, kvheads,
+                             head_dim, block_size, num_blocks, eps)
+        self.distinct(out, [qkv, kcache, vcache, positions, seq_indices, block_tables, rope_cache])
+        for cache in (kcache, vcache):
+            self.distinct(cache, [rope_cache, seq_indices, block_tables])
+        _check(self.lib.nv_attention_qkv_rope(self.handle, qkv.ptr, qweight.ptr, kweight.ptr, positions.ptr,
+                                              slots.ptr, kcache.ptr, vcache.ptr, seq_indices.ptr, block_tables.ptr,
+                                              out.ptr, _dimension(rows), _dimension(qheads), _dimension(kvheads),
+                                              _dimension(head_dim), _dimension(block_size), _dimension(num_blocks),
+                                              _dimension(table_stride), _dimension(batch_size),
+                                              _dimension(max_context), eps, rope_cache.ptr,
+                                              _dimension(max_positions)))
 
     def kv_write(self, k: Buffer, v: Buffer, slots: Buffer, kcache: Buffer, vcache: Buffer, rows: int,
                  kvheads: int, head_dim: int, block_size: int, num_blocks: int) -> None:

@@ -528,6 +528,65 @@ def test_attention_aligned_blocks_with_holes_mid_context(gpu):
     _attention_case(gpu, 235, pos, seqs, 16, 8, 128, bs, batch, stride, 4096, holes=holes)
 
 
+@pytest.mark.parametrize("rows,bs,seed", [(8, 256, 300), (32, 256, 310), (8, 16, 320), (5, 7, 330)])
+def test_attention_qkv_rope_matches_separate_launches(gpu, rows, bs, seed):
+    """The fused decode form (q/k norm + RoPE + KV write inside the attention
+    launch) against qkv_rope_cached + paged_attention and the oracle: out and
+    both caches bit for bit. One row per sequence with the slot its table
+    gives; 8 rows take one q head per block, 32 a GQA pair; 256-, 16- and
+    7-token blocks cover the three table lookups. The last row of the 5-row
+    case has an invalid sequence and slot -1 (zero output, no KV write)."""
+    qh, kvh, dim, max_context = 16, 8, 128, 4096
+    rng = np.random.default_rng(seed)
+    batch, stride = rows, -(-max_context // bs)
+    blocks = batch * stride
+    tables = rng.permutation(blocks).astype(np.int32)
+    pos = rng.integers(0, max_context, size=rows).astype(np.int32)
+    pos[:4] = [max_context - 1, 0, bs - 1, bs][:min(4, rows)]
+    seqs = np.arange(rows, dtype=np.int32)
+    slots = (tables[seqs * stride + pos // bs] * bs + pos % bs).astype(np.int32)
+    if rows == 5:
+        seqs[-1], slots[-1] = -1, -1
+    heads = qh + 2 * kvh
+    qkv = ora.normal_bf16((rows, heads, dim), seed + 1)
+    qw = ora.normal_bf16(dim, seed + 2, 1.0, 0.02)
+    kw = ora.normal_bf16(dim, seed + 3, 1.0, 0.02)
+    kc0 = ora.normal_bf16((blocks, bs, kvh, dim), seed + 4)
+    vc0 = ora.normal_bf16((blocks, bs, kvh, dim), seed + 5)
+    tb = gpu.alloc(max_context * dim * 4)
+    gpu.rope_cache(tb, max_context, dim, THETA)
+    dq, dqw, dkw, dpos, dslots, dseqs, dtab = (up(gpu, a) for a in (qkv, qw, kw, pos, slots, seqs, tables))
+
+    kc1, vc1 = up(gpu, kc0), up(gpu, vc0)
+    qout, out1 = gpu.alloc(rows * qh * dim * 2), gpu.alloc(rows * qh * dim * 2)
+    gpu.qkv_rope_cached(dq, dqw, dkw, dpos, dslots, qout, kc1, vc1, rows, qh, kvh, dim, bs, blocks, EPS, tb,
+                        max_context)
+    gpu.paged_attention(qout, kc1, vc1, dpos, dseqs, dtab, out1, rows, qh, kvh, dim, bs, blocks, stride, batch,
+                        max_context)
+    kc2, vc2 = up(gpu, kc0), up(gpu, vc0)
+    out2 = gpu.alloc(rows * qh * dim * 2)
+    gpu.attention_qkv_rope(dq, dqw, dkw, dpos, dslots, kc2, vc2, dseqs, dtab, out2, rows, qh, kvh, dim, bs, blocks,
+                           stride, batch, max_context, EPS, tb, max_context)
+    shape = (blocks, bs, kvh, dim)
+    for name, a, b, sh in (("out", out1, out2, (rows, qh, dim)), ("k cache", kc1, kc2, shape),
+                           ("v cache", vc1, vc2, shape)):
+        assert_bits_equal(down(b, np.uint16, sh), down(a, np.uint16, sh), name)
+
+    table = down(tb, np.float32, (max_context, dim))
+    q_r, kc_r, vc_r = ora.qkv_rope(qkv, qw, kw, pos, slots, kc0, vc0, rows, qh, kvh, dim, bs, blocks, EPS,
+                                   table=table, max_positions=max_context, threads=8)
+    want = ora.attention(q_r, kc_r, vc_r, pos, seqs, tables, rows, qh, kvh, dim, bs, blocks, stride, batch,
+                         max_context, threads=8)
+    assert_bits_equal(down(out2, np.uint16, (rows, qh, dim)), want, "out vs oracle")
+    assert_bits_equal(down(kc2, np.uint16, shape), kc_r, "k cache vs oracle")
+
+
+def test_attention_qkv_rope_rejects_other_head_dims(gpu):
+    b = gpu.alloc(1 << 16)
+    with pytest.raises(Exception):
+        gpu.attention_qkv_rope(b, b, b, b, b, b, b, b, b, b, 1, 2, 1, 64, 16, 1, 1, 1, 16, EPS, b, 16)
+
+
 def test_attention_generic_path_for_unaligned_queries(gpu):
     _attention_case(gpu, 240, [0, 77, 399], [0, 1, 1], 4, 2, 128, 16, 2, 25, 400, align=False)
 
