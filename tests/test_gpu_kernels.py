@@ -625,3 +625,47 @@ def test_gemm_known_answer_and_random(gpu):
     got = f32_of(down(yb, np.uint16, (m, n))).astype(np.float64)
     want = f32_of(xa).astype(np.float64) @ f32_of(wa).astype(np.float64).T
     assert np.max(np.abs(got - want) / (np.abs(want) + 1.0)) < 1e-2
+
+
+def _gemm_bound(xa, wa):
+    """float64 product and an error bound for fp32 accumulation + one bf16
+    rounding: 2^-8 |y| + 2^-20 k sum|x w| (a dropped or doubled 8-element
+    chunk is far outside it)."""
+    xf, wf = f32_of(xa).astype(np.float64), f32_of(wa).astype(np.float64)
+    return xf @ wf.T, 2.0 ** -8 * np.abs(xf @ wf.T) + 2.0 ** -20 * xa.shape[1] * (np.abs(xf) @ np.abs(wf).T)
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 4096, 1024), (8, 1024, 2048), (8, 6144, 1024), (8, 1024, 3072),
+                                   (1, 1000, 512), (5, 77, 1536), (32, 4096, 1024), (16, 1024, 2048),
+                                   (3, 2050, 4096), (32, 300, 2048), (33, 64, 512)])
+def test_gemm_few_rows(gpu, m, n, k):
+    """Decode-sized GEMMs (the Qwen3-0.6B layer shapes at 8, 16 and 32 rows,
+    ragged n and odd row counts) against the float64 product."""
+    seed = m * 131 + n * 7 + k
+    xa = ora.normal_bf16((m, k), seed)
+    wa = ora.normal_bf16((n, k), seed + 1)
+    yb = gpu.alloc(m * n * 2)
+    gpu.gemm(up(gpu, xa), up(gpu, wa), yb, m, n, k)
+    got = f32_of(down(yb, np.uint16, (m, n))).astype(np.float64)
+    want, bound = _gemm_bound(xa, wa)
+    assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) - bound)
+
+
+def test_gemm_few_rows_graph_replays(gpu):
+    """A decode-sized GEMM captured in a graph: every replay (new X uploaded
+    between them) equals an eager launch bit for bit."""
+    m, n, k = 8, 1024, 1024
+    wa = ora.normal_bf16((n, k), 170)
+    w, x, y = up(gpu, wa), gpu.alloc(m * k * 2), gpu.alloc(m * n * 2)
+    x.upload(ora.normal_bf16((m, k), 171))
+    gpu.sync()
+    graph = gpu.capture(lambda: gpu.gemm(x, w, y, m, n, k))
+    for seed in (172, 173, 174):
+        xa = ora.normal_bf16((m, k), seed)
+        x.upload(xa)
+        graph.replay()
+        replayed = down(y, np.uint16, (m, n)).copy()
+        gpu.gemm(x, w, y, m, n, k)
+        assert_bits_equal(replayed, down(y, np.uint16, (m, n)))
+        want, bound = _gemm_bound(xa, wa)
+        assert np.all(np.abs(f32_of(replayed).astype(np.float64) - want) <= bound)
