@@ -373,6 +373,34 @@ def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain, only=()):
                                                        db * dper, dstride, db, MAX_POS) for i in range(dsets)],
                       bytes_attention(db, dctx, dstride), db))
 
+    # The decode form with q/k norm + RoPE + KV write fused into attention, at
+    # the same 8 x 1024 shape: it reads the packed qkv rows instead of q and
+    # writes each row's K and V slot (token 1023 of its sequence).
+    if want("attention_qkv_rope_decode_8x1024"):
+        fb, fctx = 8, 1024
+        fstride, fper = MAX_POS // BS, fctx // BS
+        fsets = sets_for(2 * fb * fper * BS * KVH * D * 2)
+        fkc = [fill.normal(fb * fper * BS * KVH * D * 2) for _ in range(fsets)]
+        fvc = [fill.normal(fb * fper * BS * KVH * D * 2) for _ in range(fsets)]
+        ftab = np.full((fb, fstride), -1, np.int32)
+        ftab[:, :fper] = np.random.default_rng(13).permutation(fb * fper).reshape(fb, fper)
+        fslots = fill.ints((ftab[:, (fctx - 1) // BS] * BS + (fctx - 1) % BS).astype(np.int32))
+        ftab = fill.ints(ftab.reshape(-1))
+        fpos = fill.ints(np.full(fb, fctx - 1, np.int32))
+        fseq = fill.ints(np.arange(fb, dtype=np.int32))
+        fqkv = fill.normal(fb * HEADS * D * 2)
+        fqn, fkn = fill.normal(D * 2, 1.0, 0.02), fill.normal(D * 2, 1.0, 0.02)
+        fout = gpu.alloc(fb * QH * D * 2)
+        # Attention's bytes with the qkv rows read in place of q, plus the
+        # K/V slot writes and one cos/sin row per sequence.
+        fbytes = bytes_attention(fb, fctx, fstride) + fb * ((HEADS - QH) * D * 2 + 2 * KVH * D * 2 + D * 4)
+        cases.append(("attention_qkv_rope_decode_8x1024", "q/k norm + RoPE + KV write fused into paged GQA attention, "
+                      "8 decode rows x 1024 context, 16/8 heads, dim 128, 256-token blocks",
+                      [lambda i=i: gpu.attention_qkv_rope(fqkv, fqn, fkn, fpos, fslots, fkc[i], fvc[i], fseq, ftab, fout,
+                                                          fb, QH, KVH, D, BS, fb * fper, fstride, fb, MAX_POS, EPS,
+                                                          chain.rope, MAX_POS) for i in range(fsets)],
+                      fbytes, fb))
+
     # Sampling 256 x 151936: rows 0-127 greedy, 128-255 Gumbel at T=0.6.
     if not want("sampling_256x151936", "sampling_greedy", "sampling_gumbel"):
         return cases
