@@ -480,25 +480,45 @@ def decode_steps(sequences: int) -> dict | None:
     return json.loads(done.stdout)
 
 
-def cpu_baseline(tokens: int, layers: int, threads: int) -> dict:
+def cpu_threads() -> tuple[int, int, int]:
+    """(threads used, hardware concurrency, CPUs in this process's affinity mask).
+    The leg uses every CPU of the affinity mask, capped at the job's CPU share
+    when the environment states one (OMP_NUM_THREADS: the GPU hosts allot 16
+    host CPUs to a one-GPU job whatever the mask shows)."""
+    hw = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = hw
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return (min(affinity, share) if share > 0 else affinity), hw, affinity
+
+
+def cpu_baseline(tokens: int, layers: int, runs: int = 5) -> dict:
+    """The oracle's multithreaded C restatement of the same step: all layers at
+    the step's token count, every layer with its own inputs (distinct buffers,
+    so no layer reads bytes another layer left in a cache), one contiguous row
+    range per thread. Median of `runs` timed steps after one warm-up layer."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as ora
 
+    threads, hw, affinity = cpu_threads()
     T = tokens
     tok = np.random.default_rng(0).integers(0, V, T).astype(np.int32)
     table = ora.normal_bf16((V, H), 1, 0.0, 0.02)
-    x_attn = ora.normal_bf16((T, H), 2)
-    x_mlp = ora.normal_bf16((T, H), 3)
-    qkv = ora.normal_bf16((T, HEADS, D), 4)
-    gu = ora.normal_bf16((T, 2, I), 5, 0.0, 2.0)
+    pools = dict(attn=ora.normal_bf16((T, H), 2), mlp=ora.normal_bf16((T, H), 3),
+                 qkv=ora.normal_bf16((T, HEADS, D), 4), gu=ora.normal_bf16((T, 2, I), 5, 0.0, 2.0))
+    # Layer l's inputs: the pools rotated by l rows, each layer its own copy.
+    per_layer = [{k: np.ascontiguousarray(np.roll(v, l * 97, axis=0)) for k, v in pools.items()}
+                 for l in range(layers)]
     wn = ora.normal_bf16(H, 6, 1.0, 0.02)
     qn, kn = ora.normal_bf16(D, 7, 1.0, 0.02), ora.normal_bf16(D, 8, 1.0, 0.02)
     pos = (np.arange(T) % MAX_POS).astype(np.int32)
     blocks = -(-T // BS)
     slots = np.arange(T, dtype=np.int32)
     rope = ora.rope_cache(MAX_POS, D, THETA, threads)
-    kc = np.zeros((blocks, BS, KVH, D), np.uint16)
-    vc = np.zeros_like(kc)
+    caches = [(np.zeros((blocks, BS, KVH, D), np.uint16), np.zeros((blocks, BS, KVH, D), np.uint16))
+              for _ in range(layers)]
     lib = ora.lib()
     res = np.empty((T, H), np.uint16)
     normed = np.empty((T, H), np.uint16)
@@ -509,26 +529,28 @@ def cpu_baseline(tokens: int, layers: int, threads: int) -> dict:
     def step(nlayers):
         lib.ora_embedding(p(tok), p(table), p(res), T, H, V, threads)
         for i in range(nlayers):
+            x, (kc, vc) = per_layer[i], caches[i]
             if i == 0:
                 lib.ora_rms(p(res), p(wn), p(normed), T, H, EPS, threads)
             else:
-                lib.ora_add_rms(p(x_mlp), p(res), p(wn), p(normed), T, H, EPS, threads)
-            lib.ora_qkv_rope(p(qkv), p(qn), p(kn), p(pos), p(slots), p(query), p(kc), p(vc), T, QH, KVH, D, BS, blocks,
-                             EPS, 1.0, p(rope), MAX_POS, threads)
-            lib.ora_add_rms(p(x_attn), p(res), p(wn), p(normed), T, H, EPS, threads)
-            lib.ora_silu(p(gu), p(act), T, I, threads)
-        lib.ora_add_rms(p(x_mlp), p(res), p(wn), p(normed), T, H, EPS, threads)
+                lib.ora_add_rms(p(per_layer[i - 1]["mlp"]), p(res), p(wn), p(normed), T, H, EPS, threads)
+            lib.ora_qkv_rope(p(x["qkv"]), p(qn), p(kn), p(pos), p(slots), p(query), p(kc), p(vc), T, QH, KVH, D, BS,
+                             blocks, EPS, 1.0, p(rope), MAX_POS, threads)
+            lib.ora_add_rms(p(x["attn"]), p(res), p(wn), p(normed), T, H, EPS, threads)
+            lib.ora_silu(p(x["gu"]), p(act), T, I, threads)
+        lib.ora_add_rms(p(per_layer[nlayers - 1]["mlp"]), p(res), p(wn), p(normed), T, H, EPS, threads)
 
     step(1)  # warm-up
-    runs = []
-    for _ in range(3):
+    times = []
+    for _ in range(runs):
         t0 = time.perf_counter()
         step(layers)
-        runs.append(time.perf_counter() - t0)
-    sec = float(np.median(runs))
-    return {"value": T / sec, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle C restatement, full step ({layers} layers, T={T}; per-layer inputs shared), "
-                      f"median of {len(runs)} runs = {sec * 1e3:.1f} ms/step"}
+        times.append(time.perf_counter() - t0)
+    sec = float(np.median(times))
+    return {"value": T / sec, "unit": "tokens/s", "cores": threads, "hardware_concurrency": hw,
+            "affinity_cpus": affinity, "kind": "port",
+            "sample": f"oracle C restatement, full step ({layers} layers, T={T}, distinct per-layer inputs), "
+                      f"{threads} threads, median of {len(times)} runs = {sec * 1e3:.1f} ms/step"}
 
 
 # ------------------------------------------------------------------ main ---
@@ -598,8 +620,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu and not only:
-        threads = max(1, min(16, os.cpu_count() or 1))
-        cpu = cpu_baseline(args.tokens, LAYERS, threads)
+        cpu = cpu_baseline(args.tokens, LAYERS)
 
     line = {
         "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,

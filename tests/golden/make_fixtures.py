@@ -10,8 +10,8 @@ Reads data files shipped with nano-vllm-rs (never its source code):
       the sampled token in generation.outputs[0].token_ids[0]
 
 Outputs (committed):
-  reference_logits.npz  rows 0-4 as bf16 bits (row 4 holds an exact tie for the
-                        maximum, 16.625 at tokens 9625 and 15344), and
+  reference_logits.npz  all 20 rows as bf16 bits (row 4 holds an exact tie for
+                        the maximum, 16.625 at tokens 9625 and 15344), and
                         expected_greedy for those rows
   reference_greedy.json expected greedy token of all 20 cases plus each case's
                         maximum logit and the indices that attain it
@@ -25,7 +25,7 @@ import numpy as np
 
 REF = "/root/reference"
 HERE = os.path.dirname(os.path.abspath(__file__))
-KEEP_ROWS = [0, 1, 2, 3, 4]
+KEEP_ROWS = list(range(20))
 
 
 def main() -> None:

@@ -423,14 +423,24 @@ def test_sampling_large_batches(gpu, vocab):
 
 
 def test_sampling_reference_golden_vectors(gpu):
+    """All 20 last-position logit rows of the reference's validation run and
+    the tokens its GPU greedy sampler picked (row 4: an exact tie, lower index
+    wins), through the serial kernel, the partition path (20 rows), and the
+    row-resident path (the rows tiled to at least one per CU)."""
     import os
 
     data = np.load(os.path.join(os.path.dirname(__file__), "golden", "reference_logits.npz"))
     logits, expected = data["logits_bf16"], data["expected_greedy"]
     b, v = logits.shape
+    assert b == 20
     temps, seeds = np.zeros(b, np.float32), np.zeros(b, np.uint64)
     assert _run_sampler(gpu, logits, temps, seeds, b, v).tolist() == expected.tolist()
     assert _run_sampler(gpu, logits, temps, seeds, b, v, parallel=False).tolist() == expected.tolist()
+    reps = -(-max(256, gpu.sm_count()) // b)
+    tiled = np.tile(logits, (reps, 1))
+    n = tiled.shape[0]
+    got = _run_sampler(gpu, tiled, np.zeros(n, np.float32), np.zeros(n, np.uint64), n, v)
+    assert got.tolist() == np.tile(expected, reps).tolist()
 
 
 # -------------------------------------------------------- paged attention ---
@@ -528,13 +538,15 @@ def test_attention_aligned_blocks_with_holes_mid_context(gpu):
     _attention_case(gpu, 235, pos, seqs, 16, 8, 128, bs, batch, stride, 4096, holes=holes)
 
 
-@pytest.mark.parametrize("rows,bs,seed", [(8, 256, 300), (32, 256, 310), (8, 16, 320), (5, 7, 330)])
+@pytest.mark.parametrize("rows,bs,seed", [(8, 256, 300), (32, 256, 310), (8, 16, 320), (5, 7, 330), (32, 16, 340),
+                                         (32, 7, 350)])
 def test_attention_qkv_rope_matches_separate_launches(gpu, rows, bs, seed):
     """The fused decode form (q/k norm + RoPE + KV write inside the attention
     launch) against qkv_rope_cached + paged_attention and the oracle: out and
     both caches bit for bit. One row per sequence with the slot its table
     gives; 8 rows take one q head per block, 32 a GQA pair; 256-, 16- and
-    7-token blocks cover the three table lookups. The last row of the 5-row
+    7-token blocks cover the three table lookups (register table, shift and
+    divide), each with a GQA pair per block at 32 rows. The last row of the 5-row
     case has an invalid sequence and slot -1 (zero output, no KV write)."""
     qh, kvh, dim, max_context = 16, 8, 128, 4096
     rng = np.random.default_rng(seed)

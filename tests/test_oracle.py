@@ -343,8 +343,10 @@ def test_greedy_golden_vectors_from_reference_runs():
     # Row 4 is an exact tie for the maximum; the lower index wins.
     assert expected[4] == 9625
     summary = json.load(open(os.path.join(GOLDEN, "reference_greedy.json")))
+    assert len(summary["cases"]) == b == 20
     for case in summary["cases"]:
         assert case["expected_token"] == min(case["argmax_indices"])
+        assert expected[case["case"]] == case["expected_token"]
 
 
 def test_planted_tie_and_partitioned_equals_serial():
