@@ -168,6 +168,16 @@ int nv_sample_parallel(nv_context* c, const void* logits, const void* temps, con
 int nv_kv_write(nv_context* c, const void* k, const void* v, const void* slots, void* kc, void* vc,
                 int rows, int kvh, int dim, int bs, int blocks);
 
+/* No counterpart in the reference: nv_sample_parallel without the caller's
+ * scratch, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The partials
+ * live in a static 1 MiB device array per GPU (131072 entries of f32 score +
+ * i32 id), bound at nv_create; it calls no allocator. Returns -2 when
+ * batch * ceil(vocab / 2048) exceeds 131072. Every call on one GPU shares that
+ * array: calls that overlap on one GPU (two streams or contexts at once) race. */
+int nv_sample_parallel_static(nv_context* c, const void* logits, const void* temps, const void* seeds,
+                              void* out, int batch, int vocab);
+
 /* Per-row Gumbel seed of src/runtime.rs:780-790 (host function, no device
  * work): mix(mix(base) ^ mix(request_id) ^ mix(generated)). */
 uint64_t nv_sampling_seed(uint64_t base, uint64_t request_id, uint64_t generated);

@@ -11,6 +11,9 @@ struct nv_context {
     hipStream_t stream;
     hipblasHandle_t blas;
     int cu_count;
+    // Device address of this device's copy of the sampler's static partials
+    // (sample.hip), for nv_sample_parallel_static.
+    void* static_partials;
 };
 
 namespace nvr {
@@ -20,6 +23,10 @@ namespace nvr {
 int hip_status(hipError_t status, const char* operation);
 int blas_status(hipblasStatus_t status, const char* operation);
 int fail(int code, const char* fmt, ...);
+
+// Looks up this device's copy of the sampler's static partials (called by
+// nv_create with the context's device current).
+int bind_static_partials(nv_context* c);
 
 // Status of the most recent launch on this thread.
 inline int launch_status() { return hip_status(hipGetLastError(), "HIP kernel launch"); }

@@ -71,7 +71,7 @@ int nv_sm_count(nv_context* c, int* output) {
 
 int nv_create(int device, nv_context** output) {
     NVR_HIP(hipSetDevice(device));
-    nv_context* c = new (std::nothrow) nv_context{device, nullptr, nullptr, 0};
+    nv_context* c = new (std::nothrow) nv_context{device, nullptr, nullptr, 0, nullptr};
     if (!c) return nvr::fail(-1, "host context allocation failed");
     int error = nvr::hip_status(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking),
                                 "hipStreamCreateWithFlags");
@@ -86,6 +86,7 @@ int nv_create(int device, nv_context** output) {
     // reference's cuBLAS GEMMs do (graph replays equal eager launches).
     if (!error) error = nvr::blas_status(hipblasSetAtomicsMode(c->blas, HIPBLAS_ATOMICS_NOT_ALLOWED),
                                          "hipblasSetAtomicsMode");
+    if (!error) error = nvr::bind_static_partials(c);
     if (error) { hipblasDestroy(c->blas); (void)hipStreamDestroy(c->stream); delete c; return error; }
     *output = c;
     return 0;

@@ -671,21 +671,8 @@ int launch_resident(nv_context* c, const uint16_t* logits, const float* temps, c
     return nvr::launch_status();
 }
 
-}  // namespace
-
-extern "C" {
-
-int nv_sample(nv_context* c, const void* logits, const void* temps, const void* seeds, void* out, int batch,
-              int vocab) {
-    NVR_ACTIVATE(c);
-    if (batch <= 0 || vocab <= 0) return nvr::fail(-2, "sample: dimensions must be positive");
-    return launch_serial(c, logits, temps, seeds, out, batch, vocab);
-}
-
-int nv_sample_parallel(nv_context* c, const void* logits, const void* temps, const void* seeds, void* out,
-                       void* partial_scores, void* partial_ids, int batch, int vocab) {
-    NVR_ACTIVATE(c);
-    if (batch <= 0 || vocab <= 0) return nvr::fail(-2, "sample_parallel: dimensions must be positive");
+int launch_parallel(nv_context* c, const void* logits, const void* temps, const void* seeds, void* out,
+                    void* partial_scores, void* partial_ids, int batch, int vocab) {
     const int64_t ref_parts = (int64_t(vocab) + kRefPartition - 1) / kRefPartition;
     if (ref_parts <= 1 || int64_t(batch) * ref_parts > 0x7fffffff)
         return launch_serial(c, logits, temps, seeds, out, batch, vocab);
@@ -721,6 +708,60 @@ int nv_sample_parallel(nv_context* c, const void* logits, const void* temps, con
     NVR_HIP(hipGetLastError());
     hipLaunchKernelGGL(sample_combine, dim3(batch), dim3(64), 0, c->stream, ps, pi, static_cast<int*>(out), parts);
     return nvr::launch_status();
+}
+
+// Partials of nv_sample_parallel_static, in place of caller scratch: scores
+// (f32) in words [0, kStaticPartials), ids (i32) in [kStaticPartials,
+// 2 * kStaticPartials). 1 MiB, held by every device the library runs on
+// until the process ends. Host code must not pass `scratch` itself to a
+// kernel (in host code the name is a stand-in, not a device address): it uses
+// the address hipGetSymbolAddress gives for the current device, kept in the
+// context by bind_static_partials.
+constexpr int kStaticPartials = 1 << 17;
+static __device__ __align__(256) uint32_t scratch[2 * kStaticPartials];
+
+}  // namespace
+
+namespace nvr {
+
+int bind_static_partials(nv_context* c) {
+    void* ptr = nullptr;
+    NVR_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    c->static_partials = ptr;
+    return 0;
+}
+
+}  // namespace nvr
+
+extern "C" {
+
+int nv_sample(nv_context* c, const void* logits, const void* temps, const void* seeds, void* out, int batch,
+              int vocab) {
+    NVR_ACTIVATE(c);
+    if (batch <= 0 || vocab <= 0) return nvr::fail(-2, "sample: dimensions must be positive");
+    return launch_serial(c, logits, temps, seeds, out, batch, vocab);
+}
+
+int nv_sample_parallel(nv_context* c, const void* logits, const void* temps, const void* seeds, void* out,
+                       void* partial_scores, void* partial_ids, int batch, int vocab) {
+    NVR_ACTIVATE(c);
+    if (batch <= 0 || vocab <= 0) return nvr::fail(-2, "sample_parallel: dimensions must be positive");
+    return launch_parallel(c, logits, temps, seeds, out, partial_scores, partial_ids, batch, vocab);
+}
+
+int nv_sample_parallel_static(nv_context* c, const void* logits, const void* temps, const void* seeds, void* out,
+                              int batch, int vocab) {
+    NVR_ACTIVATE(c);
+    if (batch <= 0 || vocab <= 0) return nvr::fail(-2, "sample_parallel_static: dimensions must be positive");
+    const int64_t partials = int64_t(batch) * ((int64_t(vocab) + kRefPartition - 1) / kRefPartition);
+    if (partials > kStaticPartials)
+        return nvr::fail(-2,
+                         "sample_parallel_static: batch %d x ceil(vocab %d / 2048) = %lld partials exceed the "
+                         "static scratch of %d; use nv_sample_parallel with caller scratch",
+                         batch, vocab, (long long)partials, kStaticPartials);
+    if (!c->static_partials) return nvr::fail(-2, "sample_parallel_static: static scratch not bound");
+    auto* words = static_cast<uint32_t*>(c->static_partials);
+    return launch_parallel(c, logits, temps, seeds, out, words, words + kStaticPartials, batch, vocab);
 }
 
 }  // extern "C"

@@ -62,6 +62,7 @@ SIGNATURES = {
     "nv_gather": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "nv_sample": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i]),
     "nv_sample_parallel": (_i, [_vp] * 7 + [_i, _i]),
+    "nv_sample_parallel_static": (_i, [_vp] * 5 + [_i, _i]),
     "nv_kv_write": (_i, [_vp] * 6 + [_i] * 5),
     "nv_sampling_seed": (ctypes.c_uint64, [ctypes.c_uint64] * 3),
 }
@@ -550,6 +551,21 @@ class Gpu:
         _check(self.lib.nv_sample_parallel(self.handle, logits.ptr, temperatures.ptr, seeds.ptr, out.ptr,
                                            partial_scores.ptr, partial_ids.ptr, _dimension(batch),
                                            _dimension(vocab)))
+
+
+    STATIC_PARTIALS = 1 << 17
+
+    def sample_parallel_static(self, logits: Buffer, temperatures: Buffer, seeds: Buffer, out: Buffer, batch: int,
+                               vocab: int) -> None:
+        """sample_parallel with the library's static partials instead of caller
+        scratch (no allocation): batch * ceil(vocab / 2048) <= 131072."""
+        self.tensor(logits, [batch, vocab], 2)
+        self.tensor(temperatures, [batch], 4)
+        self.tensor(seeds, [batch], 8)
+        self.tensor(out, [batch], 4)
+        self.distinct(out, [logits, temperatures, seeds])
+        _check(self.lib.nv_sample_parallel_static(self.handle, logits.ptr, temperatures.ptr, seeds.ptr, out.ptr,
+                                                  _dimension(batch), _dimension(vocab)))
 
 
 def bf16_bits(values) -> np.ndarray:
