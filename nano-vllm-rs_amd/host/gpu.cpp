@@ -1,315 +1,340 @@
-// C++ host API over the nv_* C ABI (see gpu.hpp); the checks restate
-// src/gpu.rs:214-1146 of nano-vllm-rs.
+// C++ host API over the nv_* C ABI (contract in gpu.hpp): argument admission,
+// buffer views, graph capture and one checked method per kernel.
 #include "gpu.hpp"
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
-#include <sstream>
+#include <cstdint>
+#include <unordered_set>
 
 namespace nvr {
 
 namespace detail {
 
-struct Context {
-    nv_context* handle = nullptr;
-    bool capturing = false;
-    std::vector<Buffer> captured;  // allocations touched by the capture in progress
-
-    ~Context() {
-        if (handle) nv_destroy(handle);  // synchronises first
+// Allocations used by the kernels of the capture in progress.
+struct Recorder {
+    std::vector<std::shared_ptr<Allocation>> held;
+    std::unordered_set<const Allocation*> known;
+    void hold(const std::shared_ptr<Allocation>& a) {
+        if (known.insert(a.get()).second) held.push_back(a);
     }
-    void outside_capture() const {
-        if (capturing) throw Error("allocation, transfer and synchronization are forbidden during graph capture");
+};
+
+struct Device {
+    nv_context* ctx = nullptr;
+    std::unique_ptr<Recorder> recorder;  // non-null while a capture runs
+    ~Device() {
+        if (ctx) nv_destroy(ctx);  // waits for the stream first
     }
 };
 
 struct Allocation {
-    std::shared_ptr<Context> context;
-    void* ptr = nullptr;
-    std::size_t bytes = 0;
-
-    ~Allocation() { nv_free(context->handle, ptr); }
+    std::shared_ptr<Device> device;
+    void* base = nullptr;
+    std::size_t size = 0;
+    ~Allocation() {
+        if (base) nv_free(device->ctx, base);
+    }
 };
 
 }  // namespace detail
 
 namespace {
 
-template <class... Args>
-std::string format(const Args&... args) {
-    std::ostringstream s;
-    (s << ... << args);
-    return s.str();
+std::string str(std::size_t v) { return std::to_string(v); }
+
+// width * dims[0] * ... * dims[rank - 1], each dimension in [1, INT_MAX].
+std::size_t span_bytes(const std::size_t* dims, int rank, std::size_t width) {
+    std::size_t bytes = width;
+    for (int i = 0; i < rank; ++i) {
+        as_dim(dims[i]);
+        if (bytes > SIZE_MAX / dims[i]) throw Error(Fault::Extent, "tensor byte count overflows size_t");
+        bytes *= dims[i];
+    }
+    return bytes;
+}
+
+TensorArg make_arg(const char* name, const Buffer& b, std::size_t width, std::initializer_list<std::size_t> dims,
+                   bool written) {
+    TensorArg a{name, &b, width, {0, 0, 0, 0}, 0, written};
+    if (dims.size() > a.dims.size()) throw Error(Fault::Dimension, std::string(name) + ": more than 4 dimensions");
+    for (std::size_t d : dims) a.dims[std::size_t(a.rank++)] = d;
+    return a;
 }
 
 }  // namespace
 
-// ------------------------------------------------------------------ checks --
-void check(int status) {
-    if (status == 0) return;
-    const char* message = nv_last_error();
-    throw Error(format("HIP backend: ", message ? message : "", " (status ", status, ")"));
+const char* fault_name(Fault fault) {
+    switch (fault) {
+    case Fault::Backend: return "backend";
+    case Fault::Dimension: return "dimension";
+    case Fault::Extent: return "extent";
+    case Fault::Alignment: return "alignment";
+    case Fault::Foreign: return "foreign";
+    case Fault::Overlap: return "overlap";
+    case Fault::Value: return "value";
+    case Fault::Batch: return "batch";
+    }
+    return "?";
 }
 
-int dimension(std::size_t value) {
-    if (value == 0) throw Error("tensor dimensions must be positive");
-    if (value > std::size_t(INT_MAX)) throw Error(format("dimension ", value, " exceeds i32"));
+void require_status(int status) {
+    if (status == 0) return;
+    const char* text = nv_last_error();
+    throw Error(Fault::Backend, "libnano_hip status " + std::to_string(status) + ": " + (text ? text : ""));
+}
+
+int as_dim(std::size_t value) {
+    if (value == 0 || value > std::size_t(INT_MAX))
+        throw Error(Fault::Dimension, "dimension " + str(value) + " outside [1, 2^31 - 1]");
     return int(value);
 }
 
-std::size_t extent(std::initializer_list<std::size_t> dims, std::size_t element_size) {
-    std::size_t n = element_size;
-    for (std::size_t d : dims) {
-        dimension(d);
-        if (n > SIZE_MAX / d) throw Error("tensor byte count overflow");
-        n *= d;
-    }
-    return n;
+std::size_t byte_count(std::initializer_list<std::size_t> dims, std::size_t width) {
+    if (dims.size() > 8) throw Error(Fault::Dimension, "more than 8 dimensions");
+    std::size_t d[8];
+    int rank = 0;
+    for (std::size_t v : dims) d[rank++] = v;
+    return span_bytes(d, rank, width);
 }
 
-void positive(float value, const char* name) {
-    if (!(std::isfinite(value) && value > 0.0f)) throw Error(format(name, " must be positive and finite"));
+void require_positive(float value, const char* what) {
+    if (!(value > 0.0f) || !std::isfinite(value))
+        throw Error(Fault::Value, std::string(what) + " = " + std::to_string(value) + ", not a positive finite number");
 }
 
-void heads(std::size_t qheads, std::size_t kvheads, std::size_t head_dim) {
-    dimension(qheads);
-    dimension(kvheads);
-    dimension(head_dim);
-    if (qheads % kvheads != 0) throw Error("query heads must be a multiple of KV heads");
-    if (head_dim % 2 != 0 || head_dim > 256) throw Error("head dimension must be even and at most 256");
-    if (qheads + kvheads > 65535) throw Error("too many heads for one launch");
+void require_head_layout(std::size_t qheads, std::size_t kvheads, std::size_t head_dim) {
+    as_dim(qheads);
+    as_dim(kvheads);
+    as_dim(head_dim);
+    if (qheads % kvheads != 0)
+        throw Error(Fault::Value, str(qheads) + " query heads do not group evenly over " + str(kvheads) + " KV heads");
+    if (head_dim % 2 != 0 || head_dim > 256)
+        throw Error(Fault::Value, "head_dim " + str(head_dim) + " is not an even number up to 256");
+    if (qheads + kvheads > 65535)
+        throw Error(Fault::Value, str(qheads + kvheads) + " q + KV heads exceed one launch's 65535 grid rows");
+}
+
+TensorArg read_arg(const char* name, const Buffer& b, std::size_t width, std::initializer_list<std::size_t> dims) {
+    return make_arg(name, b, width, dims, false);
+}
+TensorArg write_arg(const char* name, const Buffer& b, std::size_t width, std::initializer_list<std::size_t> dims) {
+    return make_arg(name, b, width, dims, true);
 }
 
 // ------------------------------------------------------------------ Buffer --
-void* Buffer::ptr() const { return static_cast<char*>(allocation_->ptr) + offset_; }
-
-void Buffer::bounds(std::size_t bytes) const {
-    if (bytes > bytes_) throw Error(format("buffer needs ", bytes, " bytes, allocation has ", bytes_));
-}
+void* Buffer::address() const { return static_cast<char*>(allocation_->base) + offset_; }
 
 Buffer Buffer::slice(std::size_t offset, std::size_t bytes) const {
-    if (offset > SIZE_MAX - bytes) throw Error("buffer view extent overflow");
-    bounds(offset + bytes);
-    if (offset_ > SIZE_MAX - offset) throw Error("buffer view offset overflow");
-    const std::size_t start = offset_ + offset;
-    if (start > allocation_->bytes || bytes > allocation_->bytes - start) throw Error("buffer view exceeds allocation");
-    return Buffer(allocation_, start, bytes);
+    // This view lies inside its allocation, so a sub-range of it does too.
+    if (offset > length_ || bytes > length_ - offset)
+        throw Error(Fault::Extent, "sub-view [" + str(offset) + ", +" + str(bytes) + ") of a " + str(length_) +
+                                       "-byte view");
+    return Buffer(allocation_, offset_ + offset, bytes);
 }
 
 bool Buffer::overlaps(const Buffer& other) const {
-    return bytes_ > 0 && other.bytes_ > 0 && allocation_ == other.allocation_ &&
-           offset_ < other.offset_ + other.bytes_ && other.offset_ < offset_ + bytes_;
+    if (!allocation_ || allocation_ != other.allocation_ || length_ == 0 || other.length_ == 0) return false;
+    return std::max(offset_, other.offset_) < std::min(offset_ + length_, other.offset_ + other.length_);
 }
 
-void Buffer::upload(const void* data, std::size_t bytes) const {
-    allocation_->context->outside_capture();
-    bounds(bytes);
-    if (bytes == 0) return;
-    check(nv_upload(allocation_->context->handle, ptr(), data, bytes));  // synchronises
+void Buffer::write(const void* data, std::size_t bytes) const {
+    if (bytes > length_) throw Error(Fault::Extent, "upload of " + str(bytes) + " bytes into a " + str(length_) + "-byte view");
+    if (bytes != 0) require_status(nv_upload(allocation_->device->ctx, address(), data, bytes));
 }
 
-void Buffer::download_into(void* data, std::size_t bytes) const {
-    allocation_->context->outside_capture();
-    bounds(bytes);
-    if (bytes == 0) return;
-    check(nv_download(allocation_->context->handle, ptr(), data, bytes));  // synchronises
+void Buffer::read(void* data, std::size_t bytes) const {
+    if (bytes != 0) require_status(nv_download(allocation_->device->ctx, address(), data, bytes));
 }
 
 // ------------------------------------------------------------------- Graph --
-Graph::Graph(std::shared_ptr<detail::Context> context, void* handle, std::vector<Buffer> buffers)
-    : context_(std::move(context)), handle_(handle), buffers_(std::move(buffers)) {}
+Graph::Graph(std::shared_ptr<detail::Device> device, void* exec, std::vector<std::shared_ptr<detail::Allocation>> held)
+    : device_(std::move(device)), exec_(exec), held_(std::move(held)) {}
+
+void Graph::release() noexcept {
+    if (exec_) nv_graph_destroy(device_->ctx, exec_);
+    exec_ = nullptr;
+}
 
 Graph::Graph(Graph&& other) noexcept
-    : context_(std::move(other.context_)), handle_(other.handle_), buffers_(std::move(other.buffers_)) {
-    other.handle_ = nullptr;
-}
+    : device_(std::move(other.device_)), exec_(std::exchange(other.exec_, nullptr)), held_(std::move(other.held_)) {}
 
 Graph& Graph::operator=(Graph&& other) noexcept {
     if (this != &other) {
-        if (handle_) nv_graph_destroy(context_->handle, handle_);
-        context_ = std::move(other.context_);
-        handle_ = other.handle_;
-        buffers_ = std::move(other.buffers_);
-        other.handle_ = nullptr;
+        release();
+        device_ = std::move(other.device_);
+        exec_ = std::exchange(other.exec_, nullptr);
+        held_ = std::move(other.held_);
     }
     return *this;
 }
 
-Graph::~Graph() {
-    if (handle_) nv_graph_destroy(context_->handle, handle_);
-}
+Graph::~Graph() { release(); }
 
 void Graph::replay() const {
-    context_->outside_capture();
-    check(nv_graph_replay(context_->handle, handle_));
+    if (!exec_) throw Error(Fault::Value, "replay of an empty graph");
+    require_status(nv_graph_replay(device_->ctx, exec_));
 }
 
 // --------------------------------------------------------------------- Gpu --
 Gpu::Gpu(int device) {
-    if (device < 0) throw Error("device index must be nonnegative");
+    if (device < 0) throw Error(Fault::Value, "device index " + std::to_string(device) + " is negative");
     nv_context* ctx = nullptr;
-    check(nv_create(device, &ctx));
-    if (!ctx) throw Error("the backend returned a null context");
-    context_ = std::make_shared<detail::Context>();
-    context_->handle = ctx;
+    require_status(nv_create(device, &ctx));
+    device_ = std::make_shared<detail::Device>();
+    device_->ctx = ctx;
 }
 
-nv_context* Gpu::handle() const { return context_->handle; }
+nv_context* Gpu::context() const { return device_->ctx; }
 
 Buffer Gpu::alloc(std::size_t bytes) const {
-    context_->outside_capture();
-    if (bytes == 0 || bytes > std::size_t(PTRDIFF_MAX)) throw Error(format("invalid allocation size ", bytes));
-    void* ptr = nullptr;
-    check(nv_alloc(handle(), bytes, &ptr));
-    if (!ptr) throw Error("the backend returned a null allocation");
-    auto allocation = std::make_shared<detail::Allocation>();
-    allocation->context = context_;
-    allocation->ptr = ptr;
-    allocation->bytes = bytes;
-    return Buffer(std::move(allocation), 0, bytes);
+    if (bytes == 0 || bytes > std::size_t(PTRDIFF_MAX)) throw Error(Fault::Extent, "allocation of " + str(bytes) + " bytes");
+    void* base = nullptr;
+    require_status(nv_alloc(context(), bytes, &base));
+    auto a = std::make_shared<detail::Allocation>();
+    a->device = device_;
+    a->base = base;
+    a->size = bytes;
+    return Buffer(std::move(a), 0, bytes);
 }
 
-void Gpu::sync() const {
-    context_->outside_capture();
-    check(nv_sync(handle()));
-}
+void Gpu::sync() const { require_status(nv_sync(context())); }
 
 std::pair<std::size_t, std::size_t> Gpu::mem_info() const {
-    context_->outside_capture();
     std::size_t free_bytes = 0, total = 0;
-    check(nv_mem_info(handle(), &free_bytes, &total));
+    require_status(nv_mem_info(context(), &free_bytes, &total));
     return {free_bytes, total};
 }
 
 std::size_t Gpu::sm_count() const {
     int n = 0;
-    check(nv_sm_count(handle(), &n));
-    if (n <= 0) throw Error("invalid compute unit count");
-    return std::size_t(n);
-}
-
-void Gpu::tensor(const Buffer& buffer, std::initializer_list<std::size_t> dims, std::size_t element_size) const {
-    if (buffer.allocation_->context != context_) throw Error("buffer belongs to a different context");
-    buffer.bounds(extent(dims, element_size));
-    if (buffer.offset_ % element_size != 0) throw Error("tensor view is not aligned to its element size");
-    if (context_->capturing) {
-        for (const Buffer& b : context_->captured)
-            if (b.allocation_ == buffer.allocation_) return;
-        context_->captured.push_back(buffer);
-    }
-}
-
-void Gpu::distinct(const Buffer& output, std::initializer_list<const Buffer*> inputs) {
-    for (const Buffer* input : inputs)
-        if (output.overlaps(*input)) throw Error("kernel output aliases an input or another output");
+    require_status(nv_sm_count(context(), &n));
+    return std::size_t(as_dim(std::size_t(std::max(n, 0))));
 }
 
 Graph Gpu::capture(const std::function<void()>& forward) const {
-    context_->outside_capture();
-    check(nv_capture_begin(handle()));
-    context_->capturing = true;
-    struct Guard {  // ends an interrupted capture exactly once
-        detail::Context* context;
-        bool active = true;
-        ~Guard() {
-            if (!active) return;
-            nv_capture_abort(context->handle);
-            context->capturing = false;
-            context->captured.clear();
+    detail::Device& d = *device_;
+    if (d.recorder) throw Error(Fault::Value, "a capture is already running on this Gpu");
+    require_status(nv_capture_begin(d.ctx));
+    d.recorder = std::make_unique<detail::Recorder>();
+    try {
+        forward();
+    } catch (...) {
+        nv_capture_abort(d.ctx);
+        d.recorder.reset();
+        throw;
+    }
+    void* exec = nullptr;
+    const int status = nv_capture_end(d.ctx, &exec);  // the capture is over whatever the status
+    std::unique_ptr<detail::Recorder> rec = std::move(d.recorder);
+    require_status(status);
+    return Graph(device_, exec, std::move(rec->held));
+}
+
+void Gpu::admit(const char* op, std::initializer_list<TensorArg> args) const {
+    struct Span {
+        const detail::Allocation* allocation;
+        std::size_t begin, end;
+    };
+    std::vector<Span> spans;
+    spans.reserve(args.size());
+    for (const TensorArg& a : args) {
+        const Buffer& b = *a.buffer;
+        const std::string who = std::string(op) + ": argument '" + a.name + "'";
+        if (!b.allocation_ || b.allocation_->device != device_)
+            throw Error(Fault::Foreign, who + " was not allocated by this Gpu");
+        const std::size_t need = span_bytes(a.dims.data(), a.rank, a.width);
+        if (need > b.length_)
+            throw Error(Fault::Extent, who + " needs " + str(need) + " bytes; its view holds " + str(b.length_));
+        if (b.offset_ % a.width != 0)
+            throw Error(Fault::Alignment, who + " starts at byte " + str(b.offset_) + ", not a multiple of " +
+                                              str(a.width));
+        spans.push_back({b.allocation_.get(), b.offset_, b.offset_ + need});
+    }
+    std::size_t i = 0;
+    for (const TensorArg& a : args) {
+        if (a.written) {
+            std::size_t j = 0;
+            for (const TensorArg& other : args) {
+                const Span& x = spans[i];
+                const Span& y = spans[j];
+                if (j != i && x.allocation == y.allocation && std::max(x.begin, y.begin) < std::min(x.end, y.end))
+                    throw Error(Fault::Overlap, std::string(op) + ": written argument '" + a.name +
+                                                    "' shares bytes with argument '" + other.name + "'");
+                ++j;
+            }
         }
-    } guard{context_.get()};
-    forward();
-    void* graph = nullptr;
-    const int status = nv_capture_end(handle(), &graph);  // consumes the capture, also on failure
-    guard.active = false;
-    context_->capturing = false;
-    std::vector<Buffer> buffers = std::move(context_->captured);
-    context_->captured.clear();
-    check(status);
-    if (!graph) throw Error("the backend returned a null graph");
-    return Graph(context_, graph, std::move(buffers));
+        ++i;
+    }
+    if (device_->recorder)
+        for (const TensorArg& a : args) device_->recorder->hold(a.buffer->allocation_);
 }
 
 // ----------------------------------------------------------------- kernels --
 void Gpu::gemm(const Buffer& x, const Buffer& w, const Buffer& y, std::size_t m, std::size_t n,
                std::size_t k) const {
-    tensor(x, {m, k}, 2);
-    tensor(w, {n, k}, 2);
-    tensor(y, {m, n}, 2);
-    distinct(y, {&x, &w});
-    check(nv_gemm(handle(), x.ptr(), w.ptr(), y.ptr(), dimension(m), dimension(n), dimension(k)));
+    admit("gemm", {read_arg("x", x, 2, {m, k}), read_arg("w", w, 2, {n, k}), write_arg("y", y, 2, {m, n})});
+    require_status(nv_gemm(context(), x.address(), w.address(), y.address(), as_dim(m), as_dim(n), as_dim(k)));
 }
 
 void Gpu::embedding(const Buffer& tokens, const Buffer& weight, const Buffer& out, std::size_t rows,
                     std::size_t hidden, std::size_t vocab) const {
-    tensor(tokens, {rows}, 4);
-    tensor(weight, {vocab, hidden}, 2);
-    tensor(out, {rows, hidden}, 2);
-    distinct(out, {&tokens, &weight});
-    check(nv_embedding(handle(), tokens.ptr(), weight.ptr(), out.ptr(), dimension(rows), dimension(hidden),
-                       dimension(vocab)));
+    admit("embedding", {read_arg("tokens", tokens, 4, {rows}), read_arg("weight", weight, 2, {vocab, hidden}),
+                        write_arg("out", out, 2, {rows, hidden})});
+    require_status(nv_embedding(context(), tokens.address(), weight.address(), out.address(), as_dim(rows),
+                                as_dim(hidden), as_dim(vocab)));
 }
 
 void Gpu::rms_norm(const Buffer& x, const Buffer& weight, const Buffer& out, std::size_t rows, std::size_t hidden,
                    float eps) const {
-    positive(eps, "RMS epsilon");
-    tensor(x, {rows, hidden}, 2);
-    tensor(weight, {hidden}, 2);
-    tensor(out, {rows, hidden}, 2);
-    distinct(out, {&x, &weight});
-    check(nv_rms(handle(), x.ptr(), weight.ptr(), out.ptr(), dimension(rows), dimension(hidden), eps));
+    require_positive(eps, "rms_norm eps");
+    admit("rms_norm", {read_arg("x", x, 2, {rows, hidden}), read_arg("weight", weight, 2, {hidden}),
+                       write_arg("out", out, 2, {rows, hidden})});
+    require_status(nv_rms(context(), x.address(), weight.address(), out.address(), as_dim(rows), as_dim(hidden), eps));
 }
 
 void Gpu::add_rms_norm(const Buffer& x, const Buffer& residual, const Buffer& weight, const Buffer& out,
                        std::size_t rows, std::size_t hidden, float eps) const {
-    positive(eps, "RMS epsilon");
-    tensor(x, {rows, hidden}, 2);
-    tensor(residual, {rows, hidden}, 2);
-    tensor(weight, {hidden}, 2);
-    tensor(out, {rows, hidden}, 2);
-    distinct(out, {&x, &residual, &weight});
-    distinct(residual, {&x, &weight});
-    check(nv_add_rms(handle(), x.ptr(), residual.ptr(), weight.ptr(), out.ptr(), dimension(rows), dimension(hidden),
-                     eps));
+    require_positive(eps, "add_rms_norm eps");
+    admit("add_rms_norm", {read_arg("x", x, 2, {rows, hidden}), write_arg("residual", residual, 2, {rows, hidden}),
+                           read_arg("weight", weight, 2, {hidden}), write_arg("out", out, 2, {rows, hidden})});
+    require_status(nv_add_rms(context(), x.address(), residual.address(), weight.address(), out.address(),
+                              as_dim(rows), as_dim(hidden), eps));
 }
 
-void Gpu::check_qkv_rope(const Buffer& qkv, const Buffer& qweight, const Buffer& kweight, const Buffer& positions,
-                         const Buffer& slots, const Buffer& qout, const Buffer& kcache, const Buffer& vcache,
-                         std::size_t rows, std::size_t qheads, std::size_t kvheads, std::size_t head_dim,
-                         std::size_t block_size, std::size_t num_blocks, float eps) const {
-    heads(qheads, kvheads, head_dim);
-    positive(eps, "RMS epsilon");
-    if (kvheads > SIZE_MAX / 2 || qheads > SIZE_MAX - 2 * kvheads) throw Error("head count overflow");
-    tensor(qkv, {rows, qheads + 2 * kvheads, head_dim}, 2);
-    tensor(qweight, {head_dim}, 2);
-    tensor(kweight, {head_dim}, 2);
-    tensor(positions, {rows}, 4);
-    tensor(slots, {rows}, 4);
-    tensor(qout, {rows, qheads, head_dim}, 2);
-    tensor(kcache, {num_blocks, block_size, kvheads, head_dim}, 2);
-    tensor(vcache, {num_blocks, block_size, kvheads, head_dim}, 2);
-    for (const Buffer* out : {&qout, &kcache, &vcache}) distinct(*out, {&qkv, &qweight, &kweight, &positions, &slots});
-    distinct(qout, {&kcache, &vcache});
-    distinct(kcache, {&vcache});
-}
+namespace {
+// The arguments shared by the q/k norm + RoPE + KV write kernels.
+struct RopeShape {
+    std::size_t rows, qheads, kvheads, head_dim, block_size, num_blocks;
+    std::size_t heads() const { return qheads + 2 * kvheads; }
+};
+}  // namespace
 
 void Gpu::qkv_rope(const Buffer& qkv, const Buffer& qweight, const Buffer& kweight, const Buffer& positions,
                    const Buffer& slots, const Buffer& qout, const Buffer& kcache, const Buffer& vcache,
                    std::size_t rows, std::size_t qheads, std::size_t kvheads, std::size_t head_dim,
                    std::size_t block_size, std::size_t num_blocks, float eps, float theta) const {
-    positive(theta, "RoPE theta");
-    check_qkv_rope(qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows, qheads, kvheads, head_dim,
-                   block_size, num_blocks, eps);
-    check(nv_qkv_rope(handle(), qkv.ptr(), qweight.ptr(), kweight.ptr(), positions.ptr(), slots.ptr(), qout.ptr(),
-                      kcache.ptr(), vcache.ptr(), dimension(rows), dimension(qheads), dimension(kvheads),
-                      dimension(head_dim), dimension(block_size), dimension(num_blocks), eps, theta));
+    require_positive(eps, "qkv_rope eps");
+    require_positive(theta, "qkv_rope theta");
+    require_head_layout(qheads, kvheads, head_dim);
+    const RopeShape s{rows, qheads, kvheads, head_dim, block_size, num_blocks};
+    admit("qkv_rope", {read_arg("qkv", qkv, 2, {rows, s.heads(), head_dim}), read_arg("qweight", qweight, 2, {head_dim}),
+                       read_arg("kweight", kweight, 2, {head_dim}), read_arg("positions", positions, 4, {rows}),
+                       read_arg("slots", slots, 4, {rows}), write_arg("qout", qout, 2, {rows, qheads, head_dim}),
+                       write_arg("kcache", kcache, 2, {num_blocks, block_size, kvheads, head_dim}),
+                       write_arg("vcache", vcache, 2, {num_blocks, block_size, kvheads, head_dim})});
+    require_status(nv_qkv_rope(context(), qkv.address(), qweight.address(), kweight.address(), positions.address(),
+                               slots.address(), qout.address(), kcache.address(), vcache.address(), as_dim(rows),
+                               as_dim(qheads), as_dim(kvheads), as_dim(head_dim), as_dim(block_size),
+                               as_dim(num_blocks), eps, theta));
 }
 
 void Gpu::rope_cache(const Buffer& cache, std::size_t max_positions, std::size_t head_dim, float theta) const {
-    heads(1, 1, head_dim);
-    positive(theta, "RoPE theta");
-    tensor(cache, {max_positions, head_dim}, 4);
-    check(nv_rope_cache(handle(), cache.ptr(), dimension(max_positions), dimension(head_dim), theta));
+    require_positive(theta, "rope_cache theta");
+    require_head_layout(1, 1, head_dim);
+    admit("rope_cache", {write_arg("cache", cache, 4, {max_positions, head_dim})});
+    require_status(nv_rope_cache(context(), cache.address(), as_dim(max_positions), as_dim(head_dim), theta));
 }
 
 void Gpu::qkv_rope_cached(const Buffer& qkv, const Buffer& qweight, const Buffer& kweight, const Buffer& positions,
@@ -317,35 +342,48 @@ void Gpu::qkv_rope_cached(const Buffer& qkv, const Buffer& qweight, const Buffer
                           std::size_t rows, std::size_t qheads, std::size_t kvheads, std::size_t head_dim,
                           std::size_t block_size, std::size_t num_blocks, float eps, const Buffer& rope_cache,
                           std::size_t max_positions) const {
-    check_qkv_rope(qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows, qheads, kvheads, head_dim,
-                   block_size, num_blocks, eps);
-    tensor(rope_cache, {max_positions, head_dim}, 4);
-    for (const Buffer* out : {&qout, &kcache, &vcache}) distinct(*out, {&rope_cache});
-    check(nv_qkv_rope_cached(handle(), qkv.ptr(), qweight.ptr(), kweight.ptr(), positions.ptr(), slots.ptr(),
-                             qout.ptr(), kcache.ptr(), vcache.ptr(), dimension(rows), dimension(qheads),
-                             dimension(kvheads), dimension(head_dim), dimension(block_size), dimension(num_blocks),
-                             eps, rope_cache.ptr(), dimension(max_positions)));
+    require_positive(eps, "qkv_rope_cached eps");
+    require_head_layout(qheads, kvheads, head_dim);
+    const RopeShape s{rows, qheads, kvheads, head_dim, block_size, num_blocks};
+    admit("qkv_rope_cached",
+          {read_arg("qkv", qkv, 2, {rows, s.heads(), head_dim}), read_arg("qweight", qweight, 2, {head_dim}),
+           read_arg("kweight", kweight, 2, {head_dim}), read_arg("positions", positions, 4, {rows}),
+           read_arg("slots", slots, 4, {rows}), read_arg("rope_cache", rope_cache, 4, {max_positions, head_dim}),
+           write_arg("qout", qout, 2, {rows, qheads, head_dim}),
+           write_arg("kcache", kcache, 2, {num_blocks, block_size, kvheads, head_dim}),
+           write_arg("vcache", vcache, 2, {num_blocks, block_size, kvheads, head_dim})});
+    require_status(nv_qkv_rope_cached(context(), qkv.address(), qweight.address(), kweight.address(),
+                                      positions.address(), slots.address(), qout.address(), kcache.address(),
+                                      vcache.address(), as_dim(rows), as_dim(qheads), as_dim(kvheads),
+                                      as_dim(head_dim), as_dim(block_size), as_dim(num_blocks), eps,
+                                      rope_cache.address(), as_dim(max_positions)));
 }
+
+namespace {
+void require_context_limit(std::size_t max_context) {
+    if (max_context == 0 || max_context > 4096)
+        throw Error(Fault::Value, "max_context " + std::to_string(max_context) + " outside [1, 4096]");
+}
+}  // namespace
 
 void Gpu::paged_attention(const Buffer& q, const Buffer& kcache, const Buffer& vcache, const Buffer& positions,
                           const Buffer& seq_indices, const Buffer& block_tables, const Buffer& out, std::size_t rows,
                           std::size_t qheads, std::size_t kvheads, std::size_t head_dim, std::size_t block_size,
                           std::size_t num_blocks, std::size_t table_stride, std::size_t batch_size,
                           std::size_t max_context) const {
-    heads(qheads, kvheads, head_dim);
-    if (max_context == 0 || max_context > 4096) throw Error("paged attention supports at most 4096 context tokens");
-    tensor(q, {rows, qheads, head_dim}, 2);
-    tensor(out, {rows, qheads, head_dim}, 2);
-    tensor(kcache, {num_blocks, block_size, kvheads, head_dim}, 2);
-    tensor(vcache, {num_blocks, block_size, kvheads, head_dim}, 2);
-    tensor(positions, {rows}, 4);
-    tensor(seq_indices, {rows}, 4);
-    tensor(block_tables, {batch_size, table_stride}, 4);
-    distinct(out, {&q, &kcache, &vcache, &positions, &seq_indices, &block_tables});
-    check(nv_attention(handle(), q.ptr(), kcache.ptr(), vcache.ptr(), positions.ptr(), seq_indices.ptr(),
-                       block_tables.ptr(), out.ptr(), dimension(rows), dimension(qheads), dimension(kvheads),
-                       dimension(head_dim), dimension(block_size), dimension(num_blocks), dimension(table_stride),
-                       dimension(batch_size), dimension(max_context)));
+    require_head_layout(qheads, kvheads, head_dim);
+    require_context_limit(max_context);
+    admit("paged_attention",
+          {read_arg("q", q, 2, {rows, qheads, head_dim}),
+           read_arg("kcache", kcache, 2, {num_blocks, block_size, kvheads, head_dim}),
+           read_arg("vcache", vcache, 2, {num_blocks, block_size, kvheads, head_dim}),
+           read_arg("positions", positions, 4, {rows}), read_arg("seq_indices", seq_indices, 4, {rows}),
+           read_arg("block_tables", block_tables, 4, {batch_size, table_stride}),
+           write_arg("out", out, 2, {rows, qheads, head_dim})});
+    require_status(nv_attention(context(), q.address(), kcache.address(), vcache.address(), positions.address(),
+                                seq_indices.address(), block_tables.address(), out.address(), as_dim(rows),
+                                as_dim(qheads), as_dim(kvheads), as_dim(head_dim), as_dim(block_size),
+                                as_dim(num_blocks), as_dim(table_stride), as_dim(batch_size), as_dim(max_context)));
 }
 
 void Gpu::attention_qkv_rope(const Buffer& qkv, const Buffer& qweight, const Buffer& kweight,
@@ -355,86 +393,89 @@ void Gpu::attention_qkv_rope(const Buffer& qkv, const Buffer& qweight, const Buf
                              std::size_t head_dim, std::size_t block_size, std::size_t num_blocks,
                              std::size_t table_stride, std::size_t batch_size, std::size_t max_context, float eps,
                              const Buffer& rope_cache, std::size_t max_positions) const {
-    if (head_dim != 128) throw Error("fused attention needs head_dim 128");
-    if (max_context == 0 || max_context > 4096) throw Error("paged attention supports at most 4096 context tokens");
-    tensor(out, {rows, qheads, head_dim}, 2);
-    tensor(seq_indices, {rows}, 4);
-    tensor(block_tables, {batch_size, table_stride}, 4);
-    tensor(rope_cache, {max_positions, head_dim}, 4);
-    // The q/k norm + RoPE prologue reads and writes what qkv_rope_cached does
-    // (qout is not written: q stays on chip).
-    check_qkv_rope(qkv, qweight, kweight, positions, slots, out, kcache, vcache, rows, qheads, kvheads, head_dim,
-                   block_size, num_blocks, eps);
-    distinct(out, {&qkv, &kcache, &vcache, &positions, &seq_indices, &block_tables, &rope_cache});
-    for (const Buffer* cache : {&kcache, &vcache}) distinct(*cache, {&rope_cache, &seq_indices, &block_tables});
-    check(nv_attention_qkv_rope(handle(), qkv.ptr(), qweight.ptr(), kweight.ptr(), positions.ptr(), slots.ptr(),
-                                kcache.ptr(), vcache.ptr(), seq_indices.ptr(), block_tables.ptr(), out.ptr(),
-                                dimension(rows), dimension(qheads), dimension(kvheads), dimension(head_dim),
-                                dimension(block_size), dimension(num_blocks), dimension(table_stride),
-                                dimension(batch_size), dimension(max_context), eps, rope_cache.ptr(),
-                                dimension(max_positions)));
+    require_positive(eps, "attention_qkv_rope eps");
+    require_head_layout(qheads, kvheads, head_dim);
+    if (head_dim != 128) throw Error(Fault::Value, "attention_qkv_rope takes head_dim 128 only");
+    require_context_limit(max_context);
+    const RopeShape s{rows, qheads, kvheads, head_dim, block_size, num_blocks};
+    admit("attention_qkv_rope",
+          {read_arg("qkv", qkv, 2, {rows, s.heads(), head_dim}), read_arg("qweight", qweight, 2, {head_dim}),
+           read_arg("kweight", kweight, 2, {head_dim}), read_arg("positions", positions, 4, {rows}),
+           read_arg("slots", slots, 4, {rows}), read_arg("seq_indices", seq_indices, 4, {rows}),
+           read_arg("block_tables", block_tables, 4, {batch_size, table_stride}),
+           read_arg("rope_cache", rope_cache, 4, {max_positions, head_dim}),
+           write_arg("kcache", kcache, 2, {num_blocks, block_size, kvheads, head_dim}),
+           write_arg("vcache", vcache, 2, {num_blocks, block_size, kvheads, head_dim}),
+           write_arg("out", out, 2, {rows, qheads, head_dim})});
+    require_status(nv_attention_qkv_rope(context(), qkv.address(), qweight.address(), kweight.address(),
+                                         positions.address(), slots.address(), kcache.address(), vcache.address(),
+                                         seq_indices.address(), block_tables.address(), out.address(), as_dim(rows),
+                                         as_dim(qheads), as_dim(kvheads), as_dim(head_dim), as_dim(block_size),
+                                         as_dim(num_blocks), as_dim(table_stride), as_dim(batch_size),
+                                         as_dim(max_context), eps, rope_cache.address(), as_dim(max_positions)));
 }
 
 void Gpu::silu_mul(const Buffer& gateup, const Buffer& out, std::size_t rows, std::size_t intermediate) const {
-    tensor(gateup, {rows, 2, intermediate}, 2);
-    tensor(out, {rows, intermediate}, 2);
-    if (intermediate > std::size_t(INT_MAX) / 2) throw Error("intermediate size too large");
-    distinct(out, {&gateup});
-    check(nv_silu(handle(), gateup.ptr(), out.ptr(), dimension(rows), dimension(intermediate)));
+    if (intermediate > std::size_t(INT_MAX) / 2)
+        throw Error(Fault::Dimension, "silu_mul: 2 * intermediate exceeds 2^31 - 1");
+    admit("silu_mul", {read_arg("gateup", gateup, 2, {rows, 2, intermediate}),
+                       write_arg("out", out, 2, {rows, intermediate})});
+    require_status(nv_silu(context(), gateup.address(), out.address(), as_dim(rows), as_dim(intermediate)));
 }
 
 void Gpu::gather(const Buffer& x, const Buffer& indices, const Buffer& out, std::size_t rows, std::size_t hidden,
                  std::size_t input_rows) const {
-    tensor(x, {input_rows, hidden}, 2);
-    tensor(indices, {rows}, 4);
-    tensor(out, {rows, hidden}, 2);
-    distinct(out, {&x, &indices});
-    check(nv_gather(handle(), x.ptr(), indices.ptr(), out.ptr(), dimension(rows), dimension(hidden),
-                    dimension(input_rows)));
+    admit("gather", {read_arg("x", x, 2, {input_rows, hidden}), read_arg("indices", indices, 4, {rows}),
+                     write_arg("out", out, 2, {rows, hidden})});
+    require_status(nv_gather(context(), x.address(), indices.address(), out.address(), as_dim(rows), as_dim(hidden),
+                             as_dim(input_rows)));
 }
 
 void Gpu::sample(const Buffer& logits, const Buffer& temperatures, const Buffer& seeds, const Buffer& out,
                  std::size_t batch, std::size_t vocab) const {
-    tensor(logits, {batch, vocab}, 2);
-    tensor(temperatures, {batch}, 4);
-    tensor(seeds, {batch}, 8);
-    tensor(out, {batch}, 4);
-    distinct(out, {&logits, &temperatures, &seeds});
-    check(nv_sample(handle(), logits.ptr(), temperatures.ptr(), seeds.ptr(), out.ptr(), dimension(batch),
-                    dimension(vocab)));
+    admit("sample", {read_arg("logits", logits, 2, {batch, vocab}), read_arg("temperatures", temperatures, 4, {batch}),
+                     read_arg("seeds", seeds, 8, {batch}), write_arg("out", out, 4, {batch})});
+    require_status(nv_sample(context(), logits.address(), temperatures.address(), seeds.address(), out.address(),
+                             as_dim(batch), as_dim(vocab)));
 }
 
 void Gpu::sample_parallel(const Buffer& logits, const Buffer& temperatures, const Buffer& seeds, const Buffer& out,
                           const Buffer& partial_scores, const Buffer& partial_ids, std::size_t batch,
                           std::size_t vocab) const {
-    tensor(logits, {batch, vocab}, 2);
-    tensor(temperatures, {batch}, 4);
-    tensor(seeds, {batch}, 8);
-    tensor(out, {batch}, 4);
     const std::size_t parts = (vocab + 2047) / 2048;
-    tensor(partial_scores, {batch, parts}, 4);
-    tensor(partial_ids, {batch, parts}, 4);
-    for (const Buffer* output : {&out, &partial_scores, &partial_ids})
-        distinct(*output, {&logits, &temperatures, &seeds});
-    distinct(out, {&partial_scores, &partial_ids});
-    distinct(partial_scores, {&partial_ids});
-    check(nv_sample_parallel(handle(), logits.ptr(), temperatures.ptr(), seeds.ptr(), out.ptr(),
-                             partial_scores.ptr(), partial_ids.ptr(), dimension(batch), dimension(vocab)));
+    admit("sample_parallel",
+          {read_arg("logits", logits, 2, {batch, vocab}), read_arg("temperatures", temperatures, 4, {batch}),
+           read_arg("seeds", seeds, 8, {batch}), write_arg("out", out, 4, {batch}),
+           write_arg("partial_scores", partial_scores, 4, {batch, parts}),
+           write_arg("partial_ids", partial_ids, 4, {batch, parts})});
+    require_status(nv_sample_parallel(context(), logits.address(), temperatures.address(), seeds.address(),
+                                      out.address(), partial_scores.address(), partial_ids.address(), as_dim(batch),
+                                      as_dim(vocab)));
+}
+
+void Gpu::sample_parallel_static(const Buffer& logits, const Buffer& temperatures, const Buffer& seeds,
+                                 const Buffer& out, std::size_t batch, std::size_t vocab) const {
+    admit("sample_parallel_static",
+          {read_arg("logits", logits, 2, {batch, vocab}), read_arg("temperatures", temperatures, 4, {batch}),
+           read_arg("seeds", seeds, 8, {batch}), write_arg("out", out, 4, {batch})});
+    require_status(nv_sample_parallel_static(context(), logits.address(), temperatures.address(), seeds.address(),
+                                             out.address(), as_dim(batch), as_dim(vocab)));
 }
 
 void Gpu::kv_write(const Buffer& k, const Buffer& v, const Buffer& slots, const Buffer& kcache, const Buffer& vcache,
                    std::size_t rows, std::size_t kvheads, std::size_t head_dim, std::size_t block_size,
                    std::size_t num_blocks) const {
-    heads(kvheads, kvheads, head_dim);
-    tensor(k, {rows, kvheads, head_dim}, 2);
-    tensor(v, {rows, kvheads, head_dim}, 2);
-    tensor(slots, {rows}, 4);
-    tensor(kcache, {num_blocks, block_size, kvheads, head_dim}, 2);
-    tensor(vcache, {num_blocks, block_size, kvheads, head_dim}, 2);
-    for (const Buffer* out : {&kcache, &vcache}) distinct(*out, {&k, &v, &slots});
-    distinct(kcache, {&vcache});
-    check(nv_kv_write(handle(), k.ptr(), v.ptr(), slots.ptr(), kcache.ptr(), vcache.ptr(), dimension(rows),
-                      dimension(kvheads), dimension(head_dim), dimension(block_size), dimension(num_blocks)));
+    as_dim(kvheads);
+    as_dim(head_dim);
+    if (kvheads > std::size_t(INT_MAX) / head_dim)
+        throw Error(Fault::Dimension, "kv_write: kvheads * head_dim exceeds 2^31 - 1");
+    admit("kv_write", {read_arg("k", k, 2, {rows, kvheads, head_dim}), read_arg("v", v, 2, {rows, kvheads, head_dim}),
+                       read_arg("slots", slots, 4, {rows}),
+                       write_arg("kcache", kcache, 2, {num_blocks, block_size, kvheads, head_dim}),
+                       write_arg("vcache", vcache, 2, {num_blocks, block_size, kvheads, head_dim})});
+    require_status(nv_kv_write(context(), k.address(), v.address(), slots.address(), kcache.address(),
+                               vcache.address(), as_dim(rows), as_dim(kvheads), as_dim(head_dim), as_dim(block_size),
+                               as_dim(num_blocks)));
 }
 
 }  // namespace nvr

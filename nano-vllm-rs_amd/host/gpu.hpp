@@ -1,16 +1,37 @@
-// C++ host API over the nv_* C ABI: the object model and argument checks of
-// nano-vllm-rs's src/gpu.rs (Gpu, Buffer, Graph; src/gpu.rs:214-1146).
+// C++ host API over the nv_* C ABI of libnano_hip.so, used by the Qwen3 runner
+// (model.hpp), decode_bench and the C++ tests.
 //
-// Ownership follows the reference: a Gpu owns one context (device, stream,
-// BLAS handle); every Buffer keeps its allocation and the context alive, and
-// views (Buffer::slice) share the allocation; a Graph keeps every buffer its
-// capture touched alive. Failures throw nvr::Error with the reference's
-// messages. Objects are not thread-safe (one context = one stream; the
-// reference's Rc types are !Send as well).
+// The class and method names follow the Rust host of nano-vllm-rs
+// (src/gpu.rs: Gpu, Buffer, Graph, one method per kernel) so that callers read
+// the same in either language. The checks are this library's own contract:
 //
-// Link with libnano_hip.so; this file needs no HIP headers.
+//  Tensor arguments. A kernel call lists its tensor arguments, each with a
+//  name, whether the kernel writes it, an element width and a shape, and one
+//  routine (Gpu::admit) checks them all before the C call:
+//    - every dimension is in [1, INT_MAX] and the byte count fits size_t
+//      (Fault::Dimension, Fault::Extent);
+//    - the view holds at least that many bytes (Fault::Extent);
+//    - the view starts at a multiple of the element width (Fault::Alignment);
+//    - the buffer was allocated by this Gpu (Fault::Foreign);
+//    - the bytes a written argument covers overlap no byte that another
+//      argument covers (Fault::Overlap): outputs alias nothing.
+//  Scalars. eps and theta must be finite and positive; q heads a multiple of
+//  KV heads, head_dim even and at most 256, q + KV heads at most 65535
+//  (Fault::Value).
+//  Capture. The library itself refuses allocation, transfers and
+//  synchronisation while its stream is being captured (status -2, surfaced
+//  as Fault::Backend). A capture here only records the allocations its
+//  kernels use, and the Graph keeps them alive.
+//
+// Memory ownership: a Buffer is a view (offset, length) of a reference-counted
+// device allocation, which in turn holds the device context; the context is
+// destroyed (after a stream synchronisation) when its last user goes. Objects
+// are single-threaded: one context is one stream.
+//
+// This header needs no HIP headers; link libnvr_host.a and libnano_hip.so.
 #pragma once
 
+#include <array>
 #include <cstddef>
 #include <cstdint>
 #include <functional>
@@ -25,62 +46,79 @@
 
 namespace nvr {
 
+// What a failure was about; tests assert on it rather than on message text.
+enum class Fault { Backend, Dimension, Extent, Alignment, Foreign, Overlap, Value, Batch };
+const char* fault_name(Fault fault);
+
 class Error : public std::runtime_error {
 public:
-    using std::runtime_error::runtime_error;
+    Error(Fault fault, const std::string& what) : std::runtime_error(what), fault_(fault) {}
+    Fault fault() const { return fault_; }
+
+private:
+    Fault fault_;
 };
 
-// Argument checks of src/gpu.rs:214-241.
-void check(int status);                                                 // non-zero -> Error with nv_last_error()
-int dimension(std::size_t value);                                       // 0 < value <= INT_MAX
-std::size_t extent(std::initializer_list<std::size_t> dims, std::size_t element_size);
-void positive(float value, const char* name);                           // finite and > 0
-void heads(std::size_t qheads, std::size_t kvheads, std::size_t head_dim);  // src/gpu.rs:643-660
+// Throws Fault::Backend carrying nv_last_error() when status != 0.
+void require_status(int status);
+// value as a kernel dimension: 1 <= value <= INT_MAX, else Fault::Dimension.
+int as_dim(std::size_t value);
+// width * prod(dims), every dimension checked by as_dim; Fault::Extent on overflow.
+std::size_t byte_count(std::initializer_list<std::size_t> dims, std::size_t width);
+// Fault::Value unless value is finite and > 0.
+void require_positive(float value, const char* what);
+// Fault::Value unless the head layout is one the kernels take (see above).
+void require_head_layout(std::size_t qheads, std::size_t kvheads, std::size_t head_dim);
 
 namespace detail {
-struct Context;
+struct Device;
 struct Allocation;
 }  // namespace detail
 
 class Buffer {
 public:
-    Buffer() = default;  // empty; holds no allocation
-    std::size_t len() const { return bytes_; }
-    bool empty() const { return bytes_ == 0; }
-    // A checked view of `bytes` bytes at `offset`; it keeps the allocation alive.
+    Buffer() = default;  // empty: no allocation
+    std::size_t len() const { return length_; }
+    bool empty() const { return length_ == 0; }
+    // A view of `bytes` bytes starting `offset` bytes into this view; it
+    // shares (and keeps alive) the allocation.
     Buffer slice(std::size_t offset, std::size_t bytes) const;
+    // True when both views have bytes in one allocation in common.
     bool overlaps(const Buffer& other) const;
 
-    void upload_bytes(const std::vector<uint8_t>& values) const { upload(values.data(), values.size()); }
-    void upload_i32(const std::vector<int32_t>& values) const { upload(values.data(), values.size() * 4); }
-    void upload_u64(const std::vector<uint64_t>& values) const { upload(values.data(), values.size() * 8); }
-    void upload_f32(const std::vector<float>& values) const { upload(values.data(), values.size() * 4); }
-    void upload_u16(const std::vector<uint16_t>& values) const { upload(values.data(), values.size() * 2); }
-    std::vector<uint8_t> download_bytes(std::size_t count) const { return download<uint8_t>(count); }
-    std::vector<int32_t> download_i32(std::size_t count) const { return download<int32_t>(count); }
-    std::vector<uint64_t> download_u64(std::size_t count) const { return download<uint64_t>(count); }
-    std::vector<float> download_f32(std::size_t count) const { return download<float>(count); }
-    std::vector<uint16_t> download_u16(std::size_t count) const { return download<uint16_t>(count); }
+    // Synchronous copies (the library waits for its stream before returning).
+    void upload_bytes(const std::vector<uint8_t>& values) const { write(values.data(), values.size()); }
+    void upload_i32(const std::vector<int32_t>& values) const { write(values.data(), values.size() * 4); }
+    void upload_u64(const std::vector<uint64_t>& values) const { write(values.data(), values.size() * 8); }
+    void upload_f32(const std::vector<float>& values) const { write(values.data(), values.size() * 4); }
+    void upload_u16(const std::vector<uint16_t>& values) const { write(values.data(), values.size() * 2); }
+    std::vector<uint8_t> download_bytes(std::size_t count) const { return fetch<uint8_t>(count); }
+    std::vector<int32_t> download_i32(std::size_t count) const { return fetch<int32_t>(count); }
+    std::vector<uint64_t> download_u64(std::size_t count) const { return fetch<uint64_t>(count); }
+    std::vector<float> download_f32(std::size_t count) const { return fetch<float>(count); }
+    std::vector<uint16_t> download_u16(std::size_t count) const { return fetch<uint16_t>(count); }
 
 private:
     friend class Gpu;
-    Buffer(std::shared_ptr<detail::Allocation> allocation, std::size_t offset, std::size_t bytes)
-        : allocation_(std::move(allocation)), offset_(offset), bytes_(bytes) {}
-    void* ptr() const;
-    void bounds(std::size_t bytes) const;
-    void upload(const void* data, std::size_t bytes) const;
-    void download_into(void* data, std::size_t bytes) const;
+    Buffer(std::shared_ptr<detail::Allocation> allocation, std::size_t offset, std::size_t length)
+        : allocation_(std::move(allocation)), offset_(offset), length_(length) {}
+    void* address() const;
+    void write(const void* data, std::size_t bytes) const;
+    void read(void* data, std::size_t bytes) const;
     template <class T>
-    std::vector<T> download(std::size_t count) const {
-        if (count > SIZE_MAX / sizeof(T)) throw Error("download byte count overflow");
+    std::vector<T> fetch(std::size_t count) const {
+        if (count > length_ / sizeof(T))
+            throw Error(Fault::Extent, "download of " + std::to_string(count) + " elements of " +
+                                           std::to_string(sizeof(T)) + " bytes from a " + std::to_string(length_) +
+                                           "-byte view");
         std::vector<T> out(count);
-        download_into(out.data(), count * sizeof(T));
+        read(out.data(), count * sizeof(T));
         return out;
     }
 
     std::shared_ptr<detail::Allocation> allocation_;
     std::size_t offset_ = 0;
-    std::size_t bytes_ = 0;
+    std::size_t length_ = 0;
 };
 
 class Graph {
@@ -94,11 +132,24 @@ public:
 
 private:
     friend class Gpu;
-    Graph(std::shared_ptr<detail::Context> context, void* handle, std::vector<Buffer> buffers);
-    std::shared_ptr<detail::Context> context_;
-    void* handle_ = nullptr;
-    std::vector<Buffer> buffers_;  // captured allocations stay alive with the graph
+    Graph(std::shared_ptr<detail::Device> device, void* exec, std::vector<std::shared_ptr<detail::Allocation>> held);
+    void release() noexcept;
+    std::shared_ptr<detail::Device> device_;
+    void* exec_ = nullptr;
+    std::vector<std::shared_ptr<detail::Allocation>> held_;  // allocations the captured kernels use
 };
+
+// One tensor argument of a kernel call, for Gpu::admit.
+struct TensorArg {
+    const char* name;
+    const Buffer* buffer;
+    std::size_t width;  // bytes per element
+    std::array<std::size_t, 4> dims;
+    int rank;
+    bool written;
+};
+TensorArg read_arg(const char* name, const Buffer& b, std::size_t width, std::initializer_list<std::size_t> dims);
+TensorArg write_arg(const char* name, const Buffer& b, std::size_t width, std::initializer_list<std::size_t> dims);
 
 class Gpu {
 public:
@@ -108,9 +159,12 @@ public:
     void sync() const;
     std::pair<std::size_t, std::size_t> mem_info() const;  // (free, total) bytes
     std::size_t sm_count() const;                          // compute units
-    // Captures the device work `forward` enqueues; allocation, transfers and
-    // synchronisation inside it throw.
+    // Records the device work `forward` enqueues into a graph.
     Graph capture(const std::function<void()>& forward) const;
+
+    // Checks every tensor argument of kernel `op` (the contract above) and,
+    // during a capture, records their allocations.
+    void admit(const char* op, std::initializer_list<TensorArg> args) const;
 
     // Y[m, n] = X[m, k] * W[n, k]^T, bf16 in/out, fp32 accumulation.
     void gemm(const Buffer& x, const Buffer& w, const Buffer& y, std::size_t m, std::size_t n, std::size_t k) const;
@@ -159,24 +213,17 @@ public:
     void sample_parallel(const Buffer& logits, const Buffer& temperatures, const Buffer& seeds, const Buffer& out,
                          const Buffer& partial_scores, const Buffer& partial_ids, std::size_t batch,
                          std::size_t vocab) const;
+    // The same without caller scratch (the library's static partials).
+    void sample_parallel_static(const Buffer& logits, const Buffer& temperatures, const Buffer& seeds,
+                                const Buffer& out, std::size_t batch, std::size_t vocab) const;
     // Standalone paged KV slot write (no Rust caller in the reference).
     void kv_write(const Buffer& k, const Buffer& v, const Buffer& slots, const Buffer& kcache, const Buffer& vcache,
                   std::size_t rows, std::size_t kvheads, std::size_t head_dim, std::size_t block_size,
                   std::size_t num_blocks) const;
 
-    // Extent, alignment and context checks of one tensor argument (and, during
-    // capture, retention of its allocation by the graph).
-    void tensor(const Buffer& buffer, std::initializer_list<std::size_t> dims, std::size_t element_size) const;
-    // Throws when `output` overlaps any of `inputs`.
-    static void distinct(const Buffer& output, std::initializer_list<const Buffer*> inputs);
-
 private:
-    nv_context* handle() const;
-    void check_qkv_rope(const Buffer& qkv, const Buffer& qweight, const Buffer& kweight, const Buffer& positions,
-                        const Buffer& slots, const Buffer& qout, const Buffer& kcache, const Buffer& vcache,
-                        std::size_t rows, std::size_t qheads, std::size_t kvheads, std::size_t head_dim,
-                        std::size_t block_size, std::size_t num_blocks, float eps) const;
-    std::shared_ptr<detail::Context> context_;
+    nv_context* context() const;
+    std::shared_ptr<detail::Device> device_;
 };
 
 // Host-side seed of src/runtime.rs:780-790.

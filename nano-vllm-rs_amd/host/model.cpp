@@ -1,342 +1,417 @@
-// Qwen3 forward runner (see model.hpp); restates src/model.rs of nano-vllm-rs.
+// Qwen3 forward runner (contract in model.hpp). The layer order and the math
+// are Qwen3's, as nano-vllm-rs runs it (src/model.rs:635-818); batch checks,
+// step records, graph keys and the observer are this library's own.
 #include "model.hpp"
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstring>
-#include <set>
-#include <sstream>
+#include <unordered_map>
+#include <unordered_set>
 
 namespace nvr {
 
 namespace {
 
-template <class... Args>
-std::string format(const Args&... args) {
-    std::ostringstream s;
-    (s << ... << args);
-    return s.str();
+std::string str(std::size_t v) { return std::to_string(v); }
+
+[[noreturn]] void reject(Reject reason, const std::string& detail) {
+    throw BatchError(reason, std::string("batch rejected (") + reject_name(reason) + "): " + detail);
 }
 
-void ensure(bool ok, const char* message) {
-    if (!ok) throw Error(message);
-}
-
-// src/model.rs:1000-1004.
-std::size_t byte_size(std::initializer_list<std::size_t> dims, std::size_t width) {
-    std::size_t n = width;
-    for (std::size_t d : dims) {
-        if (d != 0 && n > SIZE_MAX / d) throw Error("tensor byte size overflow");
-        n *= d;
-    }
-    return n;
-}
-
-std::size_t add(std::size_t a, std::size_t b, const char* what) {
-    if (a > SIZE_MAX - b) throw Error(what);
-    return a + b;
+std::size_t round_up(std::size_t v, std::size_t to) {
+    if (v > SIZE_MAX - (to - 1)) throw Error(Fault::Extent, "step record size overflows size_t");
+    return (v + to - 1) / to * to;
 }
 
 }  // namespace
 
+const char* reject_name(Reject reason) {
+    switch (reason) {
+    case Reject::Rows: return "row count";
+    case Reject::Lengths: return "per-row lengths";
+    case Reject::TableShape: return "table shape";
+    case Reject::Sequences: return "sequence count";
+    case Reject::Sampling: return "sampling lengths";
+    case Reject::Token: return "token id";
+    case Reject::SampleRow: return "sampled row";
+    case Reject::Temperature: return "temperature";
+    case Reject::Position: return "position";
+    case Reject::Sequence: return "sequence id";
+    case Reject::TableColumn: return "table column";
+    case Reject::Block: return "block";
+    case Reject::Slot: return "slot";
+    case Reject::SlotReuse: return "slot reuse";
+    case Reject::Context: return "context block";
+    }
+    return "?";
+}
+
 // ------------------------------------------------------------- config ------
 void ModelConfig::validate() const {
-    ensure(num_hidden_layers > 0 && hidden_size > 0 && intermediate_size > 0 && vocab_size > 0,
-           "model dimensions must be positive");
-    ensure(num_attention_heads > 0 && num_key_value_heads > 0 && num_attention_heads % num_key_value_heads == 0,
-           "query heads must be a positive multiple of KV heads");
-    ensure(head_dim > 0 && head_dim <= 256 && head_dim % 2 == 0, "head_dim must be even and at most 256");
-    ensure(std::isfinite(rms_norm_eps) && rms_norm_eps > 0.0f && std::isfinite(rope_theta) && rope_theta > 0.0f,
-           "RMS epsilon and RoPE theta must be positive finite values");
-    ensure(max_position_embeddings > 0 && vocab_size <= std::size_t(INT_MAX), "invalid model context or vocabulary size");
-    for (std::size_t n : {hidden_size, intermediate_size, num_hidden_layers, num_attention_heads, num_key_value_heads,
-                          max_position_embeddings})
-        ensure(n <= std::size_t(INT_MAX), "model dimensions exceed 32-bit indexing");
-    byte_size({num_attention_heads, head_dim}, 2);
+    auto fail = [](const std::string& what) { throw Error(Fault::Value, "model config: " + what); };
+    for (std::size_t v : {hidden_size, intermediate_size, num_hidden_layers, num_attention_heads,
+                          num_key_value_heads, head_dim, vocab_size, max_position_embeddings})
+        if (v == 0 || v > std::size_t(INT_MAX)) fail("a dimension is 0 or above 2^31 - 1");
+    require_head_layout(num_attention_heads, num_key_value_heads, head_dim);
+    if (!(rms_norm_eps > 0.0f) || !std::isfinite(rms_norm_eps)) fail("rms_norm_eps is not a positive finite number");
+    if (!(rope_theta > 0.0f) || !std::isfinite(rope_theta)) fail("rope_theta is not a positive finite number");
+    byte_count({num_attention_heads + 2 * num_key_value_heads, head_dim, hidden_size}, 2);
 }
 
-// --------------------------------------------------------- metadata --------
-MetadataLayout MetadataLayout::make(std::size_t tokens, std::size_t sequences, std::size_t table_stride) {
-    MetadataLayout m;
-    std::size_t cursor = 0;
-    auto segment = [&](std::size_t count, std::size_t width) {
-        Range r;
-        r.start = add(cursor, 7, "metadata alignment overflow") & ~std::size_t(7);
-        r.end = add(r.start, byte_size({count}, width), "metadata extent overflow");
-        cursor = r.end;
-        return r;
+// --------------------------------------------------------- step record -----
+StepRecord StepRecord::for_capacity(std::size_t rows, std::size_t sequences, std::size_t table_stride) {
+    StepRecord r;
+    std::size_t at = 0;
+    auto place = [&](Field& f, std::size_t count, std::size_t width) {
+        f.offset = at;
+        f.bytes = byte_count({std::max<std::size_t>(count, 1)}, width);
+        at = round_up(f.offset + f.bytes, 256);
     };
-    if (table_stride != 0 && sequences > SIZE_MAX / table_stride) throw Error("block table size overflow");
-    m.tokens = segment(tokens, 4);
-    m.positions = segment(tokens, 4);
-    m.sequences = segment(tokens, 4);
-    m.slots = segment(tokens, 4);
-    m.tables = segment(sequences * table_stride, 4);
-    m.last_indices = segment(sequences, 4);
-    m.temperatures = segment(sequences, 4);
-    m.seeds = segment(sequences, 8);
-    m.bytes = cursor;
-    return m;
+    place(r.seeds, sequences, 8);
+    place(r.tokens, rows, 4);
+    place(r.positions, rows, 4);
+    place(r.sequence_ids, rows, 4);
+    place(r.slots, rows, 4);
+    place(r.last_rows, sequences, 4);
+    if (table_stride != 0 && sequences > SIZE_MAX / table_stride)
+        throw Error(Fault::Extent, "block table entries overflow size_t");
+    place(r.tables, sequences * table_stride, 4);
+    place(r.temperatures, sequences, 4);
+    r.size = at;
+    return r;
 }
 
-void MetadataLayout::pack(std::vector<uint8_t>& staging, const Batch& batch, std::size_t sequences,
-                          std::size_t table_stride) const {
-    auto put = [&](const Range& r, std::size_t offset, const void* data, std::size_t bytes) {
-        std::memcpy(staging.data() + r.start + offset, data, bytes);
+void StepRecord::fill(std::vector<uint8_t>& host, const Batch& b, std::size_t sequences,
+                      std::size_t table_stride) const {
+    auto copy = [&](const Field& f, const void* data, std::size_t bytes) {
+        if (bytes > f.bytes) throw Error(Fault::Extent, "step record field overflow");
+        if (bytes != 0) std::memcpy(host.data() + f.offset, data, bytes);
     };
-    put(tokens, 0, batch.token_ids.data(), batch.token_ids.size() * 4);
-    put(positions, 0, batch.positions.data(), batch.positions.size() * 4);
-    put(this->sequences, 0, batch.sequence_ids.data(), batch.sequence_ids.size() * 4);
-    put(slots, 0, batch.slot_mapping.data(), batch.slot_mapping.size() * 4);
-    std::memset(staging.data() + tables.start, 0xff, sequences * table_stride * 4);
+    copy(seeds, b.seeds.data(), b.seeds.size() * 8);
+    copy(tokens, b.token_ids.data(), b.token_ids.size() * 4);
+    copy(positions, b.positions.data(), b.positions.size() * 4);
+    copy(sequence_ids, b.sequence_ids.data(), b.sequence_ids.size() * 4);
+    copy(slots, b.slot_mapping.data(), b.slot_mapping.size() * 4);
+    copy(last_rows, b.last_token_indices.data(), b.last_token_indices.size() * 4);
+    copy(temperatures, b.temperatures.data(), b.temperatures.size() * 4);
+    // Tables: each sequence's row widened to the model's stride with -1 (the
+    // attention kernels treat a negative entry as no block).
+    int32_t* table = reinterpret_cast<int32_t*>(host.data() + tables.offset);
+    std::fill(table, table + tables.bytes / 4, -1);
     for (std::size_t s = 0; s < sequences; ++s)
-        put(tables, s * table_stride * 4, batch.block_tables.data() + s * batch.table_stride, batch.table_stride * 4);
-    put(last_indices, 0, batch.last_token_indices.data(), batch.last_token_indices.size() * 4);
-    put(temperatures, 0, batch.temperatures.data(), batch.temperatures.size() * 4);
-    put(seeds, 0, batch.seeds.data(), batch.seeds.size() * 8);
+        std::copy_n(b.block_tables.begin() + std::ptrdiff_t(s * b.table_stride), b.table_stride, table + s * table_stride);
 }
 
-// ------------------------------------------------------------- model -------
+// ------------------------------------------------------------------ model --
 QwenModel::QwenModel(const ModelConfig& config, const ModelOptions& options, const WeightSource& weights)
     : config_(config), options_(options), gpu_(options.device) {
     config_.validate();
     const ModelOptions& o = options_;
-    ensure(o.block_size > 0 && o.num_blocks > 0 && o.max_batch_tokens > 0 && o.max_sequences > 0 &&
-               o.max_model_len > 0,
-           "all model capacities must be positive");
-    ensure(o.max_model_len <= config_.max_position_embeddings,
-           "max_model_len exceeds checkpoint max_position_embeddings");
-    ensure(o.max_model_len <= 4096, "this attention implementation supports max_model_len up to 4096");
-    ensure(o.max_sequences <= o.max_batch_tokens, "max_sequences must not exceed max_batch_tokens");
-    if (o.num_blocks > SIZE_MAX / o.block_size) throw Error("KV slot count overflow");
-    const std::size_t cache_slots = o.num_blocks * o.block_size;
-    ensure(cache_slots <= std::size_t(INT_MAX) && o.max_batch_tokens <= std::size_t(INT_MAX),
-           "configured capacity exceeds 32-bit indexing");
+    auto fail = [](const std::string& what) { throw Error(Fault::Value, "model options: " + what); };
+    for (std::size_t v : {o.block_size, o.num_blocks, o.max_batch_tokens, o.max_sequences, o.max_model_len})
+        if (v == 0) fail("every capacity must be at least 1");
+    if (o.max_model_len > config_.max_position_embeddings) fail("max_model_len exceeds max_position_embeddings");
+    if (o.max_model_len > 4096) fail("the attention kernels hold at most 4096 context tokens");
+    if (o.max_sequences > o.max_batch_tokens) fail("max_sequences exceeds max_batch_tokens");
+    if (o.num_blocks > std::size_t(INT_MAX) / o.block_size || o.max_batch_tokens > std::size_t(INT_MAX))
+        fail("KV slots or batch rows exceed 2^31 - 1");
     table_stride_ = (o.max_model_len + o.block_size - 1) / o.block_size;
 
     const ModelConfig& c = config_;
-    auto load = [&](const std::string& name, const std::vector<std::vector<std::size_t>>& parts,
-                    const std::vector<std::string>& names) {
-        std::vector<uint16_t> all;
-        for (std::size_t i = 0; i < parts.size(); ++i) {
+    // Uploads the concatenation of the named tensors (fused projections
+    // keep the reference's row order: q, k, v and gate, up).
+    auto upload = [&](const std::vector<std::pair<std::string, std::vector<std::size_t>>>& parts) {
+        std::vector<uint16_t> bits;
+        for (const auto& [name, shape] : parts) {
             std::size_t n = 1;
-            for (std::size_t d : parts[i]) n = byte_size({d}, n);
-            std::vector<uint16_t> bits = weights(names[i], parts[i]);
-            if (bits.size() != n)
-                throw Error(format("weight ", names[i], " has ", bits.size(), " elements; expected ", n));
-            all.insert(all.end(), bits.begin(), bits.end());
+            for (std::size_t d : shape) n *= d;
+            std::vector<uint16_t> t = weights(name, shape);
+            if (t.size() != n)
+                throw Error(Fault::Extent, "weight " + name + ": " + str(t.size()) + " elements, shape holds " + str(n));
+            bits.insert(bits.end(), t.begin(), t.end());
         }
-        if (all.empty()) throw Error(format("weight ", name, " is empty"));
-        Buffer b = gpu_.alloc(all.size() * 2);
-        b.upload_u16(all);
-        memory_.weights_bytes += all.size() * 2;
+        Buffer b = gpu_.alloc(bits.size() * 2);
+        b.upload_u16(bits);
+        memory_.weights_bytes += bits.size() * 2;
         return b;
     };
-    auto one = [&](const std::string& name, std::vector<std::size_t> shape) { return load(name, {shape}, {name}); };
-
-    embedding_ = one("model.embed_tokens.weight", {c.vocab_size, c.hidden_size});
-    final_norm_ = one("model.norm.weight", {c.hidden_size});
-    lm_head_ = c.tie_word_embeddings ? embedding_ : one("lm_head.weight", {c.vocab_size, c.hidden_size});
-    const std::size_t q_size = c.num_attention_heads * c.head_dim, kv_size = c.num_key_value_heads * c.head_dim;
-    const std::size_t cache_bytes = byte_size({cache_slots, kv_size}, 2);
+    const std::size_t h = c.hidden_size, q = c.num_attention_heads * c.head_dim, kv = c.num_key_value_heads * c.head_dim;
+    embedding_ = upload({{"model.embed_tokens.weight", {c.vocab_size, h}}});
+    final_norm_ = upload({{"model.norm.weight", {h}}});
+    lm_head_ = c.tie_word_embeddings ? embedding_ : upload({{"lm_head.weight", {c.vocab_size, h}}});
+    const std::size_t slots = o.num_blocks * o.block_size;
+    const std::size_t cache_bytes = byte_count({slots, kv}, 2);
     for (std::size_t i = 0; i < c.num_hidden_layers; ++i) {
-        const std::string p = format("model.layers.", i, ".");
-        Layer l;
-        l.input_norm = one(p + "input_layernorm.weight", {c.hidden_size});
-        l.qkv = load(p + "self_attn.qkv", {{q_size, c.hidden_size}, {kv_size, c.hidden_size}, {kv_size, c.hidden_size}},
-                     {p + "self_attn.q_proj.weight", p + "self_attn.k_proj.weight", p + "self_attn.v_proj.weight"});
-        l.q_norm = one(p + "self_attn.q_norm.weight", {c.head_dim});
-        l.k_norm = one(p + "self_attn.k_norm.weight", {c.head_dim});
-        l.attention_out = one(p + "self_attn.o_proj.weight", {c.hidden_size, q_size});
-        l.post_norm = one(p + "post_attention_layernorm.weight", {c.hidden_size});
-        l.gate_up = load(p + "mlp.gate_up", {{c.intermediate_size, c.hidden_size}, {c.intermediate_size, c.hidden_size}},
-                         {p + "mlp.gate_proj.weight", p + "mlp.up_proj.weight"});
-        l.down = one(p + "mlp.down_proj.weight", {c.hidden_size, c.intermediate_size});
+        const std::string p = "model.layers." + str(i) + ".";
+        LayerWeights l;
+        l.input_norm = upload({{p + "input_layernorm.weight", {h}}});
+        l.qkv = upload({{p + "self_attn.q_proj.weight", {q, h}},
+                        {p + "self_attn.k_proj.weight", {kv, h}},
+                        {p + "self_attn.v_proj.weight", {kv, h}}});
+        l.q_norm = upload({{p + "self_attn.q_norm.weight", {c.head_dim}}});
+        l.k_norm = upload({{p + "self_attn.k_norm.weight", {c.head_dim}}});
+        l.o_proj = upload({{p + "self_attn.o_proj.weight", {h, q}}});
+        l.post_norm = upload({{p + "post_attention_layernorm.weight", {h}}});
+        l.gate_up = upload({{p + "mlp.gate_proj.weight", {c.intermediate_size, h}},
+                            {p + "mlp.up_proj.weight", {c.intermediate_size, h}}});
+        l.down = upload({{p + "mlp.down_proj.weight", {h, c.intermediate_size}}});
         l.k_cache = gpu_.alloc(cache_bytes);
         l.v_cache = gpu_.alloc(cache_bytes);
+        memory_.kv_cache_bytes += 2 * cache_bytes;
         layers_.push_back(std::move(l));
     }
 
-    auto alloc = [&](std::initializer_list<std::size_t> dims, std::size_t width) {
-        const std::size_t bytes = byte_size(dims, width);
+    const std::size_t t = o.max_batch_tokens, s = o.max_sequences;
+    auto scratch = [&](std::initializer_list<std::size_t> dims, std::size_t width) {
+        const std::size_t bytes = byte_count(dims, width);
         memory_.workspace_bytes += bytes;
         return gpu_.alloc(bytes);
     };
-    const std::size_t t = o.max_batch_tokens, s = o.max_sequences, h = c.hidden_size;
-    layout_ = MetadataLayout::make(t, s, table_stride_);
+    record_ = StepRecord::for_capacity(t, s, table_stride_);
     Workspace& w = work_;
-    w.metadata = alloc({layout_.bytes}, 1);
-    auto view = [&](const MetadataLayout::Range& r) { return w.metadata.slice(r.start, r.size()); };
-    w.tokens = view(layout_.tokens);
-    w.positions = view(layout_.positions);
-    w.seq_indices = view(layout_.sequences);
-    w.slots = view(layout_.slots);
-    w.block_tables = view(layout_.tables);
-    w.last_indices = view(layout_.last_indices);
-    w.temperatures = view(layout_.temperatures);
-    w.seeds = view(layout_.seeds);
-    const std::size_t parts = (c.vocab_size + 2047) / 2048;
-    w.samples = alloc({s}, 4);
-    w.sample_scores = alloc({s, parts}, 4);
-    w.sample_ids = alloc({s, parts}, 4);
-    w.rope_cache = alloc({o.max_model_len, c.head_dim}, 4);
-    w.residual = alloc({t, h}, 2);
-    w.hidden = alloc({t, h}, 2);
-    w.normed = alloc({t, h}, 2);
-    w.qkv = alloc({t, q_size + 2 * kv_size}, 2);
-    w.query = alloc({t, q_size}, 2);
-    w.attention = alloc({t, q_size}, 2);
-    w.gate_up = alloc({t, 2 * c.intermediate_size}, 2);
-    w.activated = alloc({t, c.intermediate_size}, 2);
-    w.gathered = alloc({s, h}, 2);
-    w.logits = alloc({s, c.vocab_size}, 2);
-    host_metadata_.assign(layout_.bytes, 0);
+    w.record = scratch({record_.size}, 1);
+    auto field = [&](const StepRecord::Field& f) { return w.record.slice(f.offset, f.bytes); };
+    w.seeds = field(record_.seeds);
+    w.tokens = field(record_.tokens);
+    w.positions = field(record_.positions);
+    w.sequence_ids = field(record_.sequence_ids);
+    w.slots = field(record_.slots);
+    w.last_rows = field(record_.last_rows);
+    w.tables = field(record_.tables);
+    w.temperatures = field(record_.temperatures);
+    const std::size_t partials = (c.vocab_size + 2047) / 2048;
+    w.samples = scratch({s}, 4);
+    w.partial_scores = scratch({s, partials}, 4);
+    w.partial_ids = scratch({s, partials}, 4);
+    w.rope_cache = scratch({o.max_model_len, c.head_dim}, 4);
+    w.residual = scratch({t, h}, 2);
+    w.hidden = scratch({t, h}, 2);
+    w.normed = scratch({t, h}, 2);
+    w.qkv = scratch({t, q + 2 * kv}, 2);
+    w.query = scratch({t, q}, 2);
+    w.attention = scratch({t, q}, 2);
+    w.gate_up = scratch({t, 2 * c.intermediate_size}, 2);
+    w.activated = scratch({t, c.intermediate_size}, 2);
+    w.gathered = scratch({s, h}, 2);
+    w.logits = scratch({s, c.vocab_size}, 2);
+    host_record_.assign(record_.size, 0);
     gpu_.rope_cache(w.rope_cache, o.max_model_len, c.head_dim, c.rope_theta);
     gpu_.sync();
-    memory_.kv_cache_bytes = byte_size({cache_bytes, 2, c.num_hidden_layers}, 1);
 }
 
-// src/model.rs:635-818, without the FlashAttention branch.
-void QwenModel::forward(std::size_t rows, std::size_t sequences, std::size_t samples, bool fused) const {
+StepPlan QwenModel::plan(const Batch& b) const {
+    const ModelOptions& o = options_;
+    StepPlan p;
+    // Shapes.
+    p.rows = b.token_ids.size();
+    if (p.rows == 0 || p.rows > o.max_batch_tokens)
+        reject(Reject::Rows, str(p.rows) + " rows for a capacity of " + str(o.max_batch_tokens));
+    if (b.positions.size() != p.rows || b.sequence_ids.size() != p.rows || b.slot_mapping.size() != p.rows)
+        reject(Reject::Lengths, "positions, sequence ids and slots must each hold " + str(p.rows) + " entries");
+    if (b.table_stride == 0 || b.table_stride > table_stride_ || b.block_tables.size() % b.table_stride != 0)
+        reject(Reject::TableShape, str(b.block_tables.size()) + " entries in rows of " + str(b.table_stride) +
+                                       " (model stride " + str(table_stride_) + ")");
+    p.sequences = b.block_tables.size() / b.table_stride;
+    if (p.sequences == 0 || p.sequences > o.max_sequences)
+        reject(Reject::Sequences, str(p.sequences) + " table rows for a capacity of " + str(o.max_sequences));
+    p.samples = b.last_token_indices.size();
+    if (p.samples > p.sequences || b.temperatures.size() != p.samples || b.seeds.size() != p.samples)
+        reject(Reject::Sampling, str(p.samples) + " sampled rows, " + str(b.temperatures.size()) + " temperatures, " +
+                                     str(b.seeds.size()) + " seeds, " + str(p.sequences) + " sequences");
+    // Values.
+    for (int32_t token : b.token_ids)
+        if (token < 0 || std::size_t(token) >= config_.vocab_size) reject(Reject::Token, "token " + std::to_string(token));
+    for (int32_t row : b.last_token_indices)
+        if (row < 0 || std::size_t(row) >= p.rows) reject(Reject::SampleRow, "row " + std::to_string(row));
+    for (float temperature : b.temperatures)
+        if (!(temperature >= 0.0f) || !std::isfinite(temperature))
+            reject(Reject::Temperature, std::to_string(temperature));
+    // Rows against their tables: the slot a row writes is the one its table
+    // gives for its position, and no two rows write the same slot.
+    auto block_at = [&](std::size_t sequence, std::size_t column) {
+        return b.block_tables[sequence * b.table_stride + column];
+    };
+    auto is_block = [&](int32_t block) { return block >= 0 && std::size_t(block) < o.num_blocks; };
+    std::vector<long long> last_position(p.sequences, -1);
+    std::vector<std::size_t> rows_of(p.sequences, 0);
+    std::unordered_set<int64_t> written;
+    written.reserve(p.rows * 2);
+    for (std::size_t r = 0; r < p.rows; ++r) {
+        const int32_t position = b.positions[r], sequence = b.sequence_ids[r];
+        if (position < 0 || std::size_t(position) >= o.max_model_len)
+            reject(Reject::Position, "row " + str(r) + " at position " + std::to_string(position));
+        if (sequence < 0 || std::size_t(sequence) >= p.sequences)
+            reject(Reject::Sequence, "row " + str(r) + " in sequence " + std::to_string(sequence));
+        const std::size_t column = std::size_t(position) / o.block_size;
+        if (column >= b.table_stride)
+            reject(Reject::TableColumn, "row " + str(r) + " needs table column " + str(column));
+        const int32_t block = block_at(std::size_t(sequence), column);
+        if (!is_block(block)) reject(Reject::Block, "row " + str(r) + " writes through block " + std::to_string(block));
+        const int64_t slot = int64_t(block) * int64_t(o.block_size) + position % int64_t(o.block_size);
+        if (b.slot_mapping[r] != slot)
+            reject(Reject::Slot, "row " + str(r) + " has slot " + std::to_string(b.slot_mapping[r]) + ", its table gives " +
+                                     std::to_string(slot));
+        if (!written.insert(slot).second) reject(Reject::SlotReuse, "slot " + std::to_string(slot));
+        last_position[std::size_t(sequence)] = std::max<long long>(last_position[std::size_t(sequence)], position);
+        ++rows_of[std::size_t(sequence)];
+    }
+    // Every block a sequence's attention reads exists.
+    for (std::size_t s = 0; s < p.sequences; ++s)
+        for (long long column = 0; last_position[s] >= 0 && column <= last_position[s] / static_cast<long long>(o.block_size); ++column)
+            if (!is_block(block_at(s, std::size_t(column))))
+                reject(Reject::Context, "sequence " + str(s) + " column " + std::to_string(column));
+
+    // Launch choices. The fused decode attention lets rows run without waiting
+    // for each other's K/V writes, so it needs every row alone in its
+    // sequence and no row reading a block another row writes.
+    p.fused_attention = o.fuse_decode_attention && config_.head_dim == 128;
+    for (std::size_t s = 0; p.fused_attention && s < p.sequences; ++s) p.fused_attention = rows_of[s] <= 1;
+    if (p.fused_attention) {
+        std::unordered_map<int32_t, std::size_t> writer;  // block -> the row writing into it
+        for (std::size_t r = 0; r < p.rows; ++r)
+            writer.emplace(int32_t(b.slot_mapping[r] / int32_t(o.block_size)), r);
+        for (std::size_t r = 0; p.fused_attention && r < p.rows; ++r) {
+            const std::size_t s = std::size_t(b.sequence_ids[r]);
+            for (std::size_t column = 0; column <= std::size_t(b.positions[r]) / o.block_size; ++column) {
+                const auto it = writer.find(block_at(s, column));
+                if (it != writer.end() && it->second != r) {
+                    p.fused_attention = false;
+                    break;
+                }
+            }
+        }
+    }
+    p.replayable = o.graphs && b.is_decode && p.rows == p.sequences && p.samples == p.sequences;
+    return p;
+}
+
+void QwenModel::observe(Stage stage, std::size_t layer) const {
+    if (observer_ && !capturing_) {
+        gpu_.sync();
+        observer_(stage, layer);
+    }
+}
+
+void QwenModel::embed(const StepPlan& p) const {
+    gpu_.embedding(work_.tokens, embedding_, work_.residual, p.rows, config_.hidden_size, config_.vocab_size);
+    observe(Stage::Embedded);
+}
+
+// One decoder layer in Qwen3's order (src/model.rs:659-789): input norm (layer
+// 0 normalises the embedding; later layers first add the previous MLP output
+// into the residual), QKV projection, q/k norm + RoPE + KV write, paged
+// attention, output projection, post-attention add-norm, gate/up projection,
+// SiLU·up, down projection.
+void QwenModel::decoder_layer(const StepPlan& p, std::size_t i) const {
     const ModelConfig& c = config_;
     const ModelOptions& o = options_;
     const Workspace& w = work_;
-    const Gpu& g = gpu_;
-    const std::size_t q_size = c.num_attention_heads * c.head_dim;
-    const std::size_t qkv_size = q_size + 2 * c.num_key_value_heads * c.head_dim;
-    g.embedding(w.tokens, embedding_, w.residual, rows, c.hidden_size, c.vocab_size);
-    for (std::size_t i = 0; i < layers_.size(); ++i) {
-        const Layer& l = layers_[i];
-        if (i == 0)
-            g.rms_norm(w.residual, l.input_norm, w.normed, rows, c.hidden_size, c.rms_norm_eps);
-        else
-            g.add_rms_norm(w.hidden, w.residual, l.input_norm, w.normed, rows, c.hidden_size, c.rms_norm_eps);
-        g.gemm(w.normed, l.qkv, w.qkv, rows, qkv_size, c.hidden_size);
-        if (fused) {
-            g.attention_qkv_rope(w.qkv, l.q_norm, l.k_norm, w.positions, w.slots, l.k_cache, l.v_cache,
-                                 w.seq_indices, w.block_tables, w.attention, rows, c.num_attention_heads,
-                                 c.num_key_value_heads, c.head_dim, o.block_size, o.num_blocks, table_stride_,
-                                 sequences, o.max_model_len, c.rms_norm_eps, w.rope_cache, o.max_model_len);
-        } else {
-            g.qkv_rope_cached(w.qkv, l.q_norm, l.k_norm, w.positions, w.slots, w.query, l.k_cache, l.v_cache, rows,
-                              c.num_attention_heads, c.num_key_value_heads, c.head_dim, o.block_size, o.num_blocks,
-                              c.rms_norm_eps, w.rope_cache, o.max_model_len);
-            g.paged_attention(w.query, l.k_cache, l.v_cache, w.positions, w.seq_indices, w.block_tables, w.attention,
-                              rows, c.num_attention_heads, c.num_key_value_heads, c.head_dim, o.block_size,
-                              o.num_blocks, table_stride_, sequences, o.max_model_len);
-        }
-        g.gemm(w.attention, l.attention_out, w.hidden, rows, c.hidden_size, q_size);
-        g.add_rms_norm(w.hidden, w.residual, l.post_norm, w.normed, rows, c.hidden_size, c.rms_norm_eps);
-        g.gemm(w.normed, l.gate_up, w.gate_up, rows, 2 * c.intermediate_size, c.hidden_size);
-        g.silu_mul(w.gate_up, w.activated, rows, c.intermediate_size);
-        g.gemm(w.activated, l.down, w.hidden, rows, c.hidden_size, c.intermediate_size);
-    }
-    if (samples > 0) {
-        g.add_rms_norm(w.hidden, w.residual, final_norm_, w.normed, rows, c.hidden_size, c.rms_norm_eps);
-        g.gather(w.normed, w.last_indices, w.gathered, samples, c.hidden_size, rows);
-        g.gemm(w.gathered, lm_head_, w.logits, samples, c.vocab_size, c.hidden_size);
-        g.sample_parallel(w.logits, w.temperatures, w.seeds, w.samples, w.sample_scores, w.sample_ids, samples,
-                          c.vocab_size);
-    }
-}
-
-// src/model.rs:820-923.
-std::array<std::size_t, 4> QwenModel::validate_batch(const Batch& b) const {
-    const ModelOptions& o = options_;
-    const std::size_t rows = b.token_ids.size(), samples = b.last_token_indices.size();
-    ensure(rows > 0 && rows <= o.max_batch_tokens, "batch token count is outside model capacity");
-    ensure(b.positions.size() == rows && b.sequence_ids.size() == rows && b.slot_mapping.size() == rows,
-           "token metadata lengths differ");
-    ensure(b.table_stride > 0 && b.table_stride <= table_stride_ && b.block_tables.size() % b.table_stride == 0,
-           "invalid block table shape");
-    const std::size_t sequences = b.block_tables.size() / b.table_stride;
-    ensure(sequences > 0 && sequences <= o.max_sequences, "batch sequence count exceeds capacity");
-    ensure(samples <= sequences && samples == b.temperatures.size() && samples == b.seeds.size(),
-           "invalid sampling metadata lengths");
-    for (int32_t token : b.token_ids)
-        ensure(token >= 0 && std::size_t(token) < config_.vocab_size, "token id outside model vocabulary");
-    for (int32_t index : b.last_token_indices)
-        ensure(index >= 0 && std::size_t(index) < rows, "sample row outside batch");
-    for (float t : b.temperatures) ensure(std::isfinite(t) && t >= 0.0f, "temperature must be finite and nonnegative");
-    std::set<std::size_t> seen;
-    std::vector<long long> max_position(sequences, -1);
-    for (std::size_t r = 0; r < rows; ++r) {
-        const int32_t position = b.positions[r], sequence = b.sequence_ids[r];
-        ensure(position >= 0 && std::size_t(position) < o.max_model_len, "token position exceeds max_model_len");
-        ensure(sequence >= 0 && std::size_t(sequence) < sequences, "token sequence index outside block tables");
-        const std::size_t column = std::size_t(position) / o.block_size;
-        ensure(column < b.table_stride, "block table does not cover token position");
-        const int32_t block = b.block_tables[std::size_t(sequence) * b.table_stride + column];
-        ensure(block >= 0 && std::size_t(block) < o.num_blocks, "invalid physical KV block");
-        const std::size_t expected = std::size_t(block) * o.block_size + std::size_t(position) % o.block_size;
-        ensure(b.slot_mapping[r] >= 0 && std::size_t(b.slot_mapping[r]) == expected,
-               "KV slot mapping disagrees with block table");
-        ensure(seen.insert(expected).second, "two input tokens write the same KV slot");
-        max_position[sequence] = std::max<long long>(max_position[sequence], position);
-    }
-    for (std::size_t s = 0; s < sequences; ++s) {
-        if (max_position[s] < 0) continue;
-        for (std::size_t column = 0; column <= std::size_t(max_position[s]) / o.block_size; ++column) {
-            const int32_t block = b.block_tables[s * b.table_stride + column];
-            ensure(block >= 0 && std::size_t(block) < o.num_blocks, "missing KV block in causal context");
-        }
-    }
-    bool fused = config_.head_dim == 128 && rows == sequences;
-    std::map<int32_t, std::size_t> writer;  // block -> the row writing into it
-    for (std::size_t r = 0; fused && r < rows; ++r) {
-        fused = max_position[std::size_t(b.sequence_ids[r])] == b.positions[r];  // its sequence's only row
-        writer.emplace(int32_t(std::size_t(b.slot_mapping[r]) / o.block_size), r);
-    }
-    for (std::size_t r = 0; fused && r < rows; ++r) {
-        const int32_t* table = &b.block_tables[std::size_t(b.sequence_ids[r]) * b.table_stride];
-        for (std::size_t column = 0; fused && column <= std::size_t(b.positions[r]) / o.block_size; ++column) {
-            const auto it = writer.find(table[column]);
-            fused = it == writer.end() || it->second == r;
-        }
-    }
-    return {rows, sequences, samples, fused ? 1u : 0u};
-}
-
-// src/model.rs:925-987, without the FlashAttention metadata.
-std::vector<uint32_t> QwenModel::run(const Batch& batch) {
-    const auto [rows, sequences, samples, fused] = validate_batch(batch);
-    last_sample_count_ = 0;
-    layout_.pack(host_metadata_, batch, sequences, table_stride_);
-    // Upload synchronises before returning, so both eager launches and graph
-    // replays see complete input and the staging vector may be reused.
-    work_.metadata.upload_bytes(host_metadata_);
-    if (options_.graphs && batch.is_decode && rows == sequences && samples == sequences) {
-        auto it = graphs_.find(2 * rows + fused);
-        if (it == graphs_.end()) {
-            // hipBLAS may initialise state on first use of a shape: warm up
-            // before capture; the replay then rewrites the same KV slots.
-            forward(rows, sequences, samples, fused);
-            gpu_.sync();
-            Graph graph = gpu_.capture([&] { forward(rows, sequences, samples, fused); });
-            it = graphs_.emplace(2 * rows + fused, std::move(graph)).first;
-        }
-        it->second.replay();
+    const LayerWeights& l = layers_[i];
+    const std::size_t h = c.hidden_size, q = c.num_attention_heads * c.head_dim;
+    const std::size_t qkv = q + 2 * c.num_key_value_heads * c.head_dim;
+    if (i == 0)
+        gpu_.rms_norm(w.residual, l.input_norm, w.normed, p.rows, h, c.rms_norm_eps);
+    else
+        gpu_.add_rms_norm(w.hidden, w.residual, l.input_norm, w.normed, p.rows, h, c.rms_norm_eps);
+    observe(Stage::InputNorm, i);
+    gpu_.gemm(w.normed, l.qkv, w.qkv, p.rows, qkv, h);
+    observe(Stage::Qkv, i);
+    if (p.fused_attention) {
+        gpu_.attention_qkv_rope(w.qkv, l.q_norm, l.k_norm, w.positions, w.slots, l.k_cache, l.v_cache, w.sequence_ids,
+                                w.tables, w.attention, p.rows, c.num_attention_heads, c.num_key_value_heads,
+                                c.head_dim, o.block_size, o.num_blocks, table_stride_, p.sequences, o.max_model_len,
+                                c.rms_norm_eps, w.rope_cache, o.max_model_len);
     } else {
-        forward(rows, sequences, samples, fused);
+        gpu_.qkv_rope_cached(w.qkv, l.q_norm, l.k_norm, w.positions, w.slots, w.query, l.k_cache, l.v_cache, p.rows,
+                             c.num_attention_heads, c.num_key_value_heads, c.head_dim, o.block_size, o.num_blocks,
+                             c.rms_norm_eps, w.rope_cache, o.max_model_len);
+        observe(Stage::QkvRope, i);
+        gpu_.paged_attention(w.query, l.k_cache, l.v_cache, w.positions, w.sequence_ids, w.tables, w.attention, p.rows,
+                             c.num_attention_heads, c.num_key_value_heads, c.head_dim, o.block_size, o.num_blocks,
+                             table_stride_, p.sequences, o.max_model_len);
     }
-    last_sample_count_ = samples;
-    if (samples == 0) {
+    observe(Stage::Attention, i);
+    gpu_.gemm(w.attention, l.o_proj, w.hidden, p.rows, h, q);
+    observe(Stage::OutProj, i);
+    gpu_.add_rms_norm(w.hidden, w.residual, l.post_norm, w.normed, p.rows, h, c.rms_norm_eps);
+    observe(Stage::PostNorm, i);
+    gpu_.gemm(w.normed, l.gate_up, w.gate_up, p.rows, 2 * c.intermediate_size, h);
+    observe(Stage::GateUp, i);
+    gpu_.silu_mul(w.gate_up, w.activated, p.rows, c.intermediate_size);
+    observe(Stage::Activated, i);
+    gpu_.gemm(w.activated, l.down, w.hidden, p.rows, h, c.intermediate_size);
+    observe(Stage::Down, i);
+}
+
+// Final norm, the sampled rows, tied lm_head and the sampler
+// (src/model.rs:781-815).
+void QwenModel::head(const StepPlan& p) const {
+    const ModelConfig& c = config_;
+    const Workspace& w = work_;
+    gpu_.add_rms_norm(w.hidden, w.residual, final_norm_, w.normed, p.rows, c.hidden_size, c.rms_norm_eps);
+    observe(Stage::FinalNorm);
+    gpu_.gather(w.normed, w.last_rows, w.gathered, p.samples, c.hidden_size, p.rows);
+    observe(Stage::Gathered);
+    gpu_.gemm(w.gathered, lm_head_, w.logits, p.samples, c.vocab_size, c.hidden_size);
+    observe(Stage::Logits);
+    gpu_.sample_parallel(w.logits, w.temperatures, w.seeds, w.samples, w.partial_scores, w.partial_ids, p.samples,
+                         c.vocab_size);
+    observe(Stage::Sampled);
+}
+
+void QwenModel::forward(const StepPlan& p) const {
+    embed(p);
+    for (std::size_t i = 0; i < layers_.size(); ++i) decoder_layer(p, i);
+    if (p.samples > 0) head(p);
+}
+
+std::vector<uint32_t> QwenModel::run(const Batch& batch) {
+    const StepPlan p = plan(batch);
+    last_samples_ = 0;
+    record_.fill(host_record_, batch, p.sequences, table_stride_);
+    work_.record.upload_bytes(host_record_);  // synchronous: the host copy may be refilled next step
+    if (p.replayable) {
+        const auto key = std::make_pair(p.rows, p.fused_attention);
+        auto found = graphs_.find(key);
+        if (found == graphs_.end()) {
+            forward(p);  // warm-up: first use of each GEMM shape stays outside the capture
+            gpu_.sync();
+            capturing_ = true;
+            try {
+                Graph g = gpu_.capture([&] { forward(p); });
+                capturing_ = false;
+                found = graphs_.emplace(key, std::move(g)).first;
+            } catch (...) {
+                capturing_ = false;
+                throw;
+            }
+        }
+        found->second.replay();  // the replay rewrites the warm-up's KV slots with the same values
+    } else {
+        forward(p);
+    }
+    last_samples_ = p.samples;
+    if (p.samples == 0) {
         gpu_.sync();
         return {};
     }
-    std::vector<uint32_t> out;
-    for (int32_t id : work_.samples.download_i32(samples)) {
-        ensure(id >= 0 && std::size_t(id) < config_.vocab_size, "GPU sampler returned an invalid token id");
-        out.push_back(uint32_t(id));
+    std::vector<uint32_t> tokens;
+    tokens.reserve(p.samples);
+    for (int32_t id : work_.samples.download_i32(p.samples)) {
+        if (id < 0 || std::size_t(id) >= config_.vocab_size)
+            throw Error(Fault::Backend, "sampler returned token " + std::to_string(id));
+        tokens.push_back(uint32_t(id));
     }
-    return out;
+    return tokens;
 }
 
 std::vector<std::vector<float>> QwenModel::last_logits() const {
     const std::size_t v = config_.vocab_size;
-    const std::vector<uint16_t> bits = work_.logits.download_u16(last_sample_count_ * v);
-    std::vector<std::vector<float>> rows(last_sample_count_, std::vector<float>(v));
-    for (std::size_t r = 0; r < last_sample_count_; ++r)
+    const std::vector<uint16_t> bits = work_.logits.download_u16(last_samples_ * v);
+    std::vector<std::vector<float>> rows(last_samples_, std::vector<float>(v));
+    for (std::size_t r = 0; r < last_samples_; ++r)
         for (std::size_t i = 0; i < v; ++i) {
             const uint32_t u = uint32_t(bits[r * v + i]) << 16;
             std::memcpy(&rows[r][i], &u, 4);

@@ -1,24 +1,35 @@
-// Qwen3 forward over the nv_* kernels: the runner of nano-vllm-rs's
-// src/model.rs (QwenModel, Workspace, MetadataLayout, validate_batch, run) on
-// the C++ host API of gpu.hpp.
+// Qwen3 forward runner over the nv_* kernels: the C++ counterpart of
+// nano-vllm-rs's QwenModel (src/model.rs), with the same outward interface
+// (model config, runtime options, run a scheduler Batch, read the last
+// logits). Internals are this library's own:
 //
-// Persistent bf16 workspaces sized for the configured capacities, a paged KV
-// cache per layer, every per-batch input packed into one staging buffer with
-// fixed, 8-byte aligned ranges (one upload per step, and kernel pointers that
-// stay identical across graph replays), and one HIP graph per decode batch
-// size, captured on first use after a warm-up forward.
+//  - StepPlan. A batch is checked once against the contract of plan() (see
+//    Reject) and reduced to its row, sequence and sample counts and to two
+//    launch choices: whether the attention of each layer may run in its fused
+//    decode form, and whether the step may replay a captured graph.
+//  - StepRecord. All per-step host data goes to the device in one synchronous
+//    copy: one record whose arrays sit at fixed 256-byte aligned offsets
+//    (widest elements first), sized for the configured capacities, so the
+//    kernels' pointers are the same in every step and every graph replay.
+//  - Graphs. A decode step that samples every row replays the HIP graph of
+//    its (row count, attention form), captured on first use after one eager
+//    warm-up forward: hipBLAS may set up state on a shape's first use, which a
+//    capture cannot contain.
+//  - Observer. Tests may watch every stage of an eager forward and read the
+//    workspace and weights at that point (used to check the forward against
+//    the CPU oracle stage by stage).
 //
 // Weights come from a WeightSource: the reference reads them from safetensors
 // files by tensor name and shape (src/model.rs:425-517); any loader with that
-// contract plugs in here.
+// contract plugs in.
 #pragma once
 
-#include <array>
 #include <cstddef>
 #include <cstdint>
 #include <functional>
 #include <map>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "gpu.hpp"
@@ -39,10 +50,13 @@ struct ModelConfig {
     float rope_theta = 1e6f;
     bool tie_word_embeddings = true;
 
-    void validate() const;  // src/model.rs:63-140 (dimension and value checks)
+    // Throws Fault::Value for a configuration the kernels cannot run.
+    void validate() const;
 };
 
-// src/model.rs:150-173; cuda_graphs is `graphs`.
+// Runtime capacities (src/model.rs:150-173; `graphs` is the reference's
+// cuda_graphs). fuse_decode_attention = false keeps every step on the
+// separate q/k norm + RoPE and attention launches.
 struct ModelOptions {
     int device = 0;
     std::size_t block_size = 256;
@@ -51,6 +65,7 @@ struct ModelOptions {
     std::size_t max_sequences = 32;
     std::size_t max_model_len = 4096;
     bool graphs = true;
+    bool fuse_decode_attention = true;
 };
 
 // One scheduler step (src/runtime.rs:18-29): flattened rows, paged block
@@ -64,20 +79,54 @@ struct Batch {
     bool is_decode = false;
 };
 
-// Byte ranges of the packed per-step metadata (src/model.rs:269-359): each
-// segment starts 8-byte aligned; block tables are padded with -1 up to the
-// model's table stride.
-struct MetadataLayout {
-    struct Range {
-        std::size_t start = 0, end = 0;
-        std::size_t size() const { return end - start; }
-    };
-    Range tokens, positions, sequences, slots, tables, last_indices, temperatures, seeds;
-    std::size_t bytes = 0;
+// Why plan() refused a batch (BatchError::reason()).
+enum class Reject {
+    Rows,         // no rows, or more than max_batch_tokens
+    Lengths,      // positions, sequence ids or slots not one per row
+    TableShape,   // table_stride 0 or wider than the model's, or tables not whole rows
+    Sequences,    // no table row, or more than max_sequences
+    Sampling,     // more sampled rows than sequences, or temperatures / seeds not one per sampled row
+    Token,        // token id outside [0, vocab_size)
+    SampleRow,    // sampled row index outside the batch
+    Temperature,  // temperature negative, NaN or infinite
+    Position,     // position outside [0, max_model_len)
+    Sequence,     // sequence id outside the table rows
+    TableColumn,  // position / block_size beyond table_stride
+    Block,        // the table entry a row writes through is not a block of the cache
+    Slot,         // slot_mapping differs from block * block_size + position % block_size
+    SlotReuse,    // two rows write the same slot
+    Context,      // a table entry before a sequence's last position is not a block of the cache
+};
+const char* reject_name(Reject reason);
 
-    static MetadataLayout make(std::size_t tokens, std::size_t sequences, std::size_t table_stride);
-    void pack(std::vector<uint8_t>& staging, const Batch& batch, std::size_t sequences,
-              std::size_t table_stride) const;
+class BatchError : public Error {
+public:
+    BatchError(Reject reason, const std::string& what) : Error(Fault::Batch, what), reason_(reason) {}
+    Reject reason() const { return reason_; }
+
+private:
+    Reject reason_;
+};
+
+struct StepPlan {
+    std::size_t rows = 0, sequences = 0, samples = 0;
+    bool fused_attention = false;  // q/k norm + RoPE + KV write inside the attention launch
+    bool replayable = false;       // served by a captured graph
+};
+
+// Byte offsets of the arrays of one step's record in device memory.
+struct StepRecord {
+    struct Field {
+        std::size_t offset = 0, bytes = 0;
+    };
+    Field seeds, tokens, positions, sequence_ids, slots, last_rows, tables, temperatures;
+    std::size_t size = 0;
+
+    // Layout for up to `rows` rows and `sequences` table rows of `table_stride`.
+    static StepRecord for_capacity(std::size_t rows, std::size_t sequences, std::size_t table_stride);
+    // Writes `batch` into `host` (size bytes); table rows are widened to
+    // `table_stride` with -1 and unused table rows are -1.
+    void fill(std::vector<uint8_t>& host, const Batch& batch, std::size_t sequences, std::size_t table_stride) const;
 };
 
 struct ModelMemoryInfo {
@@ -88,16 +137,55 @@ struct ModelMemoryInfo {
 // match; src/model.rs:425-437).
 using WeightSource = std::function<std::vector<uint16_t>(const std::string& name, const std::vector<std::size_t>& shape)>;
 
+// Points of an eager forward an observer sees, in order; `layer` is the layer
+// index for the per-layer stages and 0 otherwise.
+enum class Stage {
+    Embedded,    // residual = embedding rows
+    InputNorm,   // normed (and residual, from layer 1) after the input (add-)RMSNorm
+    Qkv,         // qkv GEMM output
+    QkvRope,     // query and this layer's K/V caches (separate launches only)
+    Attention,   // attention output (and the caches, in the fused form)
+    OutProj,     // hidden = o-proj GEMM output
+    PostNorm,    // residual and normed after the post-attention add-RMSNorm
+    GateUp,      // gate_up GEMM output
+    Activated,   // SiLU(gate) * up
+    Down,        // hidden = down GEMM output
+    FinalNorm,   // residual and normed after the final add-RMSNorm
+    Gathered,    // the sampled rows of normed
+    Logits,      // lm_head GEMM output
+    Sampled,     // sampled token ids
+};
+using StageObserver = std::function<void(Stage stage, std::size_t layer)>;
+
+// Device buffers a test may read (Workspace::*) at an observed stage.
+struct Workspace {
+    Buffer record, tokens, positions, sequence_ids, slots, tables, last_rows, temperatures, seeds;
+    Buffer samples, partial_scores, partial_ids, rope_cache;
+    Buffer residual, hidden, normed, qkv, query, attention, gate_up, activated, gathered, logits;
+};
+struct LayerWeights {
+    Buffer input_norm, qkv, q_norm, k_norm, o_proj, post_norm, gate_up, down, k_cache, v_cache;
+};
+
 class QwenModel {
 public:
     QwenModel(const ModelConfig& config, const ModelOptions& options, const WeightSource& weights);
 
-    // Validates, uploads the packed metadata (one synchronous copy), runs the
-    // forward (as a graph replay for decode batches that sample every row),
-    // and returns the sampled token of each sampled row (src/model.rs:925-987).
+    // plan(), one record upload, the forward (a graph replay when the plan
+    // allows), and the sampled token of each sampled row.
     std::vector<uint32_t> run(const Batch& batch);
-    // bf16 logits of the last run's sampled rows, as f32 (src/model.rs:617-633).
+    // bf16 logits of the last run's sampled rows, as f32.
     std::vector<std::vector<float>> last_logits() const;
+
+    // Checks `batch` and chooses its launches; throws BatchError.
+    StepPlan plan(const Batch& batch) const;
+
+    void set_observer(StageObserver observer) { observer_ = std::move(observer); }
+    const Workspace& workspace() const { return work_; }
+    const LayerWeights& layer(std::size_t i) const { return layers_.at(i); }
+    const Buffer& embedding_weight() const { return embedding_; }
+    const Buffer& final_norm_weight() const { return final_norm_; }
+    std::size_t table_stride() const { return table_stride_; }
 
     std::size_t graph_count() const { return graphs_.size(); }
     const ModelMemoryInfo& memory_usage() const { return memory_; }
@@ -105,36 +193,27 @@ public:
     const ModelOptions& options() const { return options_; }
     const Gpu& gpu() const { return gpu_; }
 
-    // rows, sequences, samples of a valid batch (src/model.rs:820-923).
-    // {rows, sequences, samples, fused}: fused = 1 when the q/k norm + RoPE +
-    // KV write may run inside the attention launch (head dim 128, one row per
-    // sequence, and no row's context holds a block another row writes).
-    std::array<std::size_t, 4> validate_batch(const Batch& batch) const;
-
 private:
-    struct Layer {
-        Buffer input_norm, qkv, q_norm, k_norm, attention_out, post_norm, gate_up, down, k_cache, v_cache;
-    };
-    struct Workspace {
-        Buffer metadata, tokens, positions, seq_indices, slots, block_tables, last_indices, temperatures, seeds;
-        Buffer samples, sample_scores, sample_ids, rope_cache;
-        Buffer residual, hidden, normed, qkv, query, attention, gate_up, activated, gathered, logits;
-    };
-
-    void forward(std::size_t rows, std::size_t sequences, std::size_t samples, bool fused) const;
+    void forward(const StepPlan& plan) const;
+    void embed(const StepPlan& plan) const;
+    void decoder_layer(const StepPlan& plan, std::size_t i) const;
+    void head(const StepPlan& plan) const;
+    void observe(Stage stage, std::size_t layer = 0) const;
 
     ModelConfig config_;
     ModelOptions options_;
     Gpu gpu_;
     std::size_t table_stride_ = 0;
-    MetadataLayout layout_;
-    std::vector<uint8_t> host_metadata_;
-    std::vector<Layer> layers_;
+    StepRecord record_;
+    std::vector<uint8_t> host_record_;
+    std::vector<LayerWeights> layers_;
     Buffer embedding_, final_norm_, lm_head_;
     Workspace work_;
     ModelMemoryInfo memory_;
-    std::map<std::size_t, Graph> graphs_;  // 2 * decode row count + fused -> captured forward
-    std::size_t last_sample_count_ = 0;
+    std::map<std::pair<std::size_t, bool>, Graph> graphs_;  // (decode rows, fused attention) -> captured forward
+    StageObserver observer_;
+    bool capturing_ = false;
+    std::size_t last_samples_ = 0;
 };
 
 }  // namespace nvr

@@ -1,16 +1,28 @@
-"""Checked host wrapper over the nano-vllm-rs HIP library (libnano_hip.so).
+"""Python host API over libnano_hip.so (ctypes), used by the tests and bench.py.
 
-This mirrors the reference's safe FFI layer, src/gpu.rs:214-1146: the same
-`Gpu`, `Buffer` and `Graph` objects, the same method names and argument
-meaning, and the same validation before every C call (positive i32 dimensions,
-finite positive eps/theta, buffer extents and element alignment, context
-identity, no output aliasing, no allocation/transfer/sync during capture).
-Violations raise `ValueError`; a non-zero status from the library raises
-`BackendError` carrying nv_last_error() and the status, as
-`check()` at src/gpu.rs:214-221 turns them into an error.
+Class and method names follow the Rust host of nano-vllm-rs (src/gpu.rs: Gpu,
+Buffer, Graph, one method per kernel, with the same argument order). The
+argument contract is this library's own, the same one the C++ host API
+(host/gpu.hpp) enforces:
 
-The library is loaded from this directory. There is no fallback: if the
-shared object is missing, every entry point raises.
+* Tensor arguments. Every kernel method lists its tensor arguments as
+  (name, buffer, element width, shape, written?) and ``Gpu._admit`` checks
+  them together: every dimension in [1, 2^31 - 1]; the view holds the byte
+  count; the view starts at a multiple of the element width; the buffer was
+  allocated by this Gpu; the bytes a written argument covers share nothing
+  with the bytes of any other argument.
+* Scalars. eps and theta finite and positive; q heads a multiple of KV heads,
+  head_dim even and at most 256, q + KV heads at most 65535.
+* Capture. The library itself refuses allocation, transfers and
+  synchronisation while its stream is captured (status -2). A capture here
+  only records the allocations its kernels use; the Graph keeps them alive.
+
+A broken rule raises ``ArgumentError`` (a ValueError) whose ``fault`` names the
+rule: "dimension", "extent", "alignment", "foreign", "overlap" or "value". A
+non-zero library status raises ``BackendError`` with nv_last_error().
+
+The library is loaded from this directory. There is no fallback: if the shared
+object is missing, every entry point raises.
 """
 from __future__ import annotations
 
@@ -19,12 +31,13 @@ import ctypes
 import math
 import os
 import sys
-from typing import Callable, Iterable, Sequence
+from typing import Callable, Sequence
 
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libnano_hip.so")
+INT_MAX = 0x7FFFFFFF
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -68,34 +81,42 @@ SIGNATURES = {
 }
 
 _LIB = None
-_EXITING = False
+_SHUTDOWN = False
 
 
-def _mark_exiting() -> None:
-    # Runs before interpreter finalization: from here on, finalizers stop
-    # calling into the library, because module teardown destroys objects in
-    # an arbitrary order and the process exit releases device memory anyway.
-    global _EXITING
-    _EXITING = True
+def _shutting_down() -> None:
+    # Runs before interpreter finalization: from then on, finalizers make no
+    # library calls (module teardown order is arbitrary, and the process exit
+    # releases device memory anyway).
+    global _SHUTDOWN
+    _SHUTDOWN = True
 
 
-atexit.register(_mark_exiting)
+atexit.register(_shutting_down)
 
 
-def _native_ok() -> bool:
-    return not _EXITING and not sys.is_finalizing()
+def _live() -> bool:
+    return not _SHUTDOWN and not sys.is_finalizing()
 
 
 class BackendError(RuntimeError):
     """A non-zero status returned by the HIP library."""
 
     def __init__(self, message: str, status: int):
-        super().__init__(f"HIP backend: {message} (status {status})")
+        super().__init__(f"libnano_hip status {status}: {message}")
         self.status = status
 
 
+class ArgumentError(ValueError):
+    """An argument broke the host contract; ``fault`` names the rule."""
+
+    def __init__(self, fault: str, message: str):
+        super().__init__(f"{fault}: {message}")
+        self.fault = fault
+
+
 def library(path: str | None = None) -> ctypes.CDLL:
-    """Loads libnano_hip.so once and declares every C signature."""
+    """Loads libnano_hip.so (once for the default path) and declares every C signature."""
     global _LIB
     if _LIB is not None and path is None:
         return _LIB
@@ -104,39 +125,48 @@ def library(path: str | None = None) -> ctypes.CDLL:
         raise FileNotFoundError(f"{target} is missing: build it with `make -C nano-vllm-rs_amd` "
                                 "(or __graft_entry__.build()); there is no fallback path")
     lib = ctypes.CDLL(target)
-    for name, (res, args) in SIGNATURES.items():
+    for name, (restype, argtypes) in SIGNATURES.items():
         fn = getattr(lib, name)
-        fn.restype = res
-        fn.argtypes = args
+        fn.restype, fn.argtypes = restype, argtypes
     if path is None:
         _LIB = lib
     return lib
 
 
-def _check(code: int, lib: ctypes.CDLL | None = None) -> None:
-    if code != 0:
-        msg = (lib or library()).nv_last_error().decode(errors="replace")
-        raise BackendError(msg, code)
+def check_status(status: int, lib: ctypes.CDLL | None = None) -> None:
+    """Raises BackendError for a non-zero library status."""
+    if status != 0:
+        raise BackendError((lib or library()).nv_last_error().decode(errors="replace"), status)
 
 
-def _dimension(value: int) -> int:
-    if value <= 0:
-        raise ValueError("tensor dimensions must be positive")
-    if value > 0x7FFFFFFF:
-        raise ValueError(f"dimension {value} exceeds i32")
+def as_dim(value: int) -> int:
+    """value as a kernel dimension in [1, 2^31 - 1]."""
+    if not 1 <= value <= INT_MAX:
+        raise ArgumentError("dimension", f"{value} outside [1, 2^31 - 1]")
     return int(value)
 
 
-def _extent(dims: Sequence[int], element_size: int) -> int:
-    n = element_size
+def byte_count(dims: Sequence[int], width: int) -> int:
+    """width * prod(dims), every dimension checked by as_dim."""
+    n = width
     for d in dims:
-        n *= _dimension(d)
+        n *= as_dim(d)
     return n
 
 
-def _positive(value: float, name: str) -> None:
+def require_positive(value: float, what: str) -> None:
     if not (math.isfinite(value) and value > 0.0):
-        raise ValueError(f"{name} must be positive and finite")
+        raise ArgumentError("value", f"{what} = {value} is not a positive finite number")
+
+
+def require_head_layout(qheads: int, kvheads: int, head_dim: int) -> None:
+    as_dim(qheads), as_dim(kvheads), as_dim(head_dim)
+    if qheads % kvheads:
+        raise ArgumentError("value", f"{qheads} query heads do not group evenly over {kvheads} KV heads")
+    if head_dim % 2 or head_dim > 256:
+        raise ArgumentError("value", f"head_dim {head_dim} is not an even number up to 256")
+    if qheads + kvheads > 65535:
+        raise ArgumentError("value", f"{qheads + kvheads} q + KV heads exceed one launch's 65535 grid rows")
 
 
 def sampling_seed(base: int, request_id: int, generated: int) -> int:
@@ -144,138 +174,131 @@ def sampling_seed(base: int, request_id: int, generated: int) -> int:
     return int(library().nv_sampling_seed(base, request_id, generated))
 
 
-class _Context:
-    def __init__(self, handle: int, lib: ctypes.CDLL):
-        self.handle = handle
-        self.capturing = False
-        self.captured: list[Buffer] = []
-        self.lib = lib
+# --------------------------------------------------------------- objects ---
+class _Device:
+    """A library context; while a capture runs, the allocations its kernels use."""
 
-    def outside_capture(self) -> None:
-        if self.capturing:
-            raise ValueError("allocation, transfer and synchronization are forbidden during graph capture")
+    def __init__(self, lib: ctypes.CDLL, ctx: int):
+        self.lib, self.ctx = lib, ctx
+        self.recording: dict[int, "_Memory"] | None = None
 
     def __del__(self):
-        if getattr(self, "handle", None) and _native_ok():
-            self.lib.nv_destroy(self.handle)
-        self.handle = None
+        if getattr(self, "ctx", None) and _live():
+            self.lib.nv_destroy(self.ctx)  # waits for the stream first
+        self.ctx = None
 
 
-class _Allocation:
-    def __init__(self, context: _Context, ptr: int, nbytes: int):
-        self.context = context
-        self.ptr = ptr
-        self.bytes = nbytes
+class _Memory:
+    """One device allocation; freed when the last view goes."""
+
+    def __init__(self, device: _Device, address: int, size: int):
+        self.device, self.address, self.size = device, address, size
 
     def __del__(self):
-        if getattr(self, "ptr", None) and _native_ok() and self.context.handle:
-            self.context.lib.nv_free(self.context.handle, self.ptr)
-        self.ptr = None
+        if getattr(self, "address", None) and _live() and self.device.ctx:
+            self.device.lib.nv_free(self.device.ctx, self.address)
+        self.address = None
 
 
 class Buffer:
-    """Owned device bytes; views share the allocation (src/gpu.rs:278-392)."""
+    """A view (offset, length) of a device allocation; views keep the allocation alive."""
 
-    def __init__(self, allocation: _Allocation, offset: int, nbytes: int):
-        self.allocation = allocation
-        self.offset = offset
-        self.bytes = nbytes
+    def __init__(self, memory: _Memory, offset: int, length: int):
+        self._memory, self._offset, self._length = memory, offset, length
 
     @property
     def ptr(self) -> int:
-        return self.allocation.ptr + self.offset
+        return self._memory.address + self._offset
+
+    @property
+    def bytes(self) -> int:
+        return self._length
 
     def __len__(self) -> int:
-        return self.bytes
-
-    def _bounds(self, nbytes: int) -> None:
-        if nbytes > self.bytes:
-            raise ValueError(f"buffer needs {nbytes} bytes, allocation has {self.bytes}")
+        return self._length
 
     def slice(self, offset: int, nbytes: int) -> "Buffer":
-        if offset < 0 or nbytes < 0:
-            raise ValueError("buffer view extent overflow")
-        self._bounds(offset + nbytes)
-        start = self.offset + offset
-        if start > self.allocation.bytes or nbytes > self.allocation.bytes - start:
-            raise ValueError("buffer view exceeds allocation")
-        return Buffer(self.allocation, start, nbytes)
+        """The sub-view [offset, offset + nbytes) of this view."""
+        if offset < 0 or nbytes < 0 or offset > self._length or nbytes > self._length - offset:
+            raise ArgumentError("extent", f"sub-view [{offset}, +{nbytes}) of a {self._length}-byte view")
+        return Buffer(self._memory, self._offset + offset, nbytes)
 
     def overlaps(self, other: "Buffer") -> bool:
-        return (self.bytes > 0 and other.bytes > 0 and self.allocation is other.allocation
-                and self.offset < other.offset + other.bytes and other.offset < self.offset + self.bytes)
+        if self._memory is not other._memory or not self._length or not other._length:
+            return False
+        return max(self._offset, other._offset) < min(self._offset + self._length, other._offset + other._length)
 
     def upload(self, values: np.ndarray) -> None:
-        ctx = self.allocation.context
-        ctx.outside_capture()
+        """Synchronous host -> device copy of `values` to the start of the view."""
         arr = np.ascontiguousarray(values)
-        self._bounds(arr.nbytes)
-        if arr.nbytes == 0:
-            return
-        _check(ctx.lib.nv_upload(ctx.handle, self.ptr, arr.ctypes.data, arr.nbytes))
+        if arr.nbytes > self._length:
+            raise ArgumentError("extent", f"upload of {arr.nbytes} bytes into a {self._length}-byte view")
+        if arr.nbytes:
+            d = self._memory.device
+            check_status(d.lib.nv_upload(d.ctx, self.ptr, arr.ctypes.data, arr.nbytes), d.lib)
 
     def download(self, dtype, count: int) -> np.ndarray:
-        ctx = self.allocation.context
-        ctx.outside_capture()
+        """Synchronous device -> host copy of `count` elements from the start of the view."""
         out = np.empty(count, dtype=dtype)
-        self._bounds(out.nbytes)
+        if out.nbytes > self._length:
+            raise ArgumentError("extent", f"download of {out.nbytes} bytes from a {self._length}-byte view")
         if out.nbytes:
-            _check(ctx.lib.nv_download(ctx.handle, self.ptr, out.ctypes.data, out.nbytes))
+            d = self._memory.device
+            check_status(d.lib.nv_download(d.ctx, self.ptr, out.ctypes.data, out.nbytes), d.lib)
         return out
 
     def download_bytes(self, count: int | None = None) -> bytes:
-        return self.download(np.uint8, self.bytes if count is None else count).tobytes()
+        return self.download(np.uint8, self._length if count is None else count).tobytes()
 
 
 class Graph:
-    """Executable graph; keeps every captured allocation alive (src/gpu.rs:1128-1146)."""
+    """An executable graph; holds the allocations its kernels use."""
 
-    def __init__(self, context: _Context, handle: int, buffers: list[Buffer]):
-        self.context = context
-        self.handle = handle
-        self._buffers = buffers
+    def __init__(self, device: _Device, exec_handle: int, held: list[_Memory]):
+        self._device, self._exec, self._held = device, exec_handle, held
 
     def replay(self) -> None:
-        self.context.outside_capture()
-        _check(self.context.lib.nv_graph_replay(self.context.handle, self.handle))
+        check_status(self._device.lib.nv_graph_replay(self._device.ctx, self._exec), self._device.lib)
 
     def __del__(self):
-        if getattr(self, "handle", None) and _native_ok() and self.context.handle:
-            self.context.lib.nv_graph_destroy(self.context.handle, self.handle)
-        self.handle = None
+        if getattr(self, "_exec", None) and _live() and self._device.ctx:
+            self._device.lib.nv_graph_destroy(self._device.ctx, self._exec)
+        self._exec = None
+
+
+def _r(name: str, buf: Buffer, width: int, *dims: int):
+    return name, buf, width, dims, False
+
+
+def _w(name: str, buf: Buffer, width: int, *dims: int):
+    return name, buf, width, dims, True
 
 
 class Gpu:
-    """One device, one stream, one hipBLAS handle (src/gpu.rs:394-1112)."""
+    """One device, one stream, one hipBLAS handle."""
 
     def __init__(self, device: int = 0, library_path: str | None = None):
         """library_path selects another build of libnano_hip.so (default: this directory's)."""
         if device < 0:
-            raise ValueError("device index must be nonnegative")
+            raise ArgumentError("value", f"device index {device} is negative")
         lib = library(library_path)
-        handle = _vp()
-        code = lib.nv_create(device, ctypes.byref(handle))
-        if code != 0:
-            raise BackendError(lib.nv_last_error().decode(errors="replace"), code)
-        if not handle.value:
-            raise BackendError("library returned a null context", -1)
-        self.context = _Context(handle.value, lib)
+        ctx = _vp()
+        check_status(lib.nv_create(device, ctypes.byref(ctx)), lib)
+        self._device = _Device(lib, ctx.value)
         self.lib = lib
 
     @property
     def handle(self) -> int:
-        return self.context.handle
+        return self._device.ctx
 
     # ------------------------------------------------------------ runtime --
     def alloc(self, nbytes: int) -> Buffer:
-        self.context.outside_capture()
+        """Zero-filled device memory."""
         if nbytes <= 0:
-            raise ValueError(f"invalid allocation size {nbytes}")
-        ptr = _vp()
-        _check(self.lib.nv_alloc(self.handle, nbytes, ctypes.byref(ptr)))
-        if not ptr.value:
-            raise BackendError("library returned a null allocation", -1)
-        return Buffer(_Allocation(self.context, ptr.value, nbytes), 0, nbytes)
+            raise ArgumentError("extent", f"allocation of {nbytes} bytes")
+        address = _vp()
+        check_status(self.lib.nv_alloc(self.handle, nbytes, ctypes.byref(address)), self.lib)
+        return Buffer(_Memory(self._device, address.value, nbytes), 0, nbytes)
 
     def upload_array(self, values: np.ndarray) -> Buffer:
         arr = np.ascontiguousarray(values)
@@ -284,274 +307,225 @@ class Gpu:
         return buf.slice(0, arr.nbytes) if arr.nbytes else buf
 
     def sync(self) -> None:
-        self.context.outside_capture()
-        _check(self.lib.nv_sync(self.handle))
+        check_status(self.lib.nv_sync(self.handle), self.lib)
 
     def mem_info(self) -> tuple[int, int]:
-        self.context.outside_capture()
         free, total = _sz(), _sz()
-        _check(self.lib.nv_mem_info(self.handle, ctypes.byref(free), ctypes.byref(total)))
+        check_status(self.lib.nv_mem_info(self.handle, ctypes.byref(free), ctypes.byref(total)), self.lib)
         return free.value, total.value
 
     def sm_count(self) -> int:
         n = _i()
-        _check(self.lib.nv_sm_count(self.handle, ctypes.byref(n)))
-        if n.value <= 0:
-            raise BackendError("invalid compute-unit count", -1)
-        return n.value
+        check_status(self.lib.nv_sm_count(self.handle, ctypes.byref(n)), self.lib)
+        return as_dim(n.value)
 
     def stream(self) -> int:
         s = _vp()
-        _check(self.lib.nv_stream(self.handle, ctypes.byref(s)))
+        check_status(self.lib.nv_stream(self.handle, ctypes.byref(s)), self.lib)
         return s.value or 0
 
-    def tensor(self, buffer: Buffer, dims: Sequence[int], element_size: int) -> None:
-        if buffer.allocation.context is not self.context:
-            raise ValueError("buffer belongs to a different context")
-        buffer._bounds(_extent(dims, element_size))
-        if buffer.offset % element_size != 0:
-            raise ValueError("tensor view is not aligned to its element size")
-        if self.context.capturing and not any(b.allocation is buffer.allocation for b in self.context.captured):
-            self.context.captured.append(buffer)
-
-    @staticmethod
-    def distinct(output: Buffer, inputs: Iterable[Buffer]) -> None:
-        if any(output.overlaps(i) for i in inputs):
-            raise ValueError("kernel output aliases an input or another output")
-
     def capture(self, forward: Callable[[], None]) -> Graph:
-        """Captures only device operations; captured buffers live with the Graph."""
-        self.context.outside_capture()
-        _check(self.lib.nv_capture_begin(self.handle))
-        self.context.capturing = True
+        """Records the device work `forward` enqueues into a graph."""
+        if self._device.recording is not None:
+            raise ArgumentError("value", "a capture is already running on this Gpu")
+        check_status(self.lib.nv_capture_begin(self.handle), self.lib)
+        self._device.recording = {}
         try:
             forward()
         except BaseException:
             self.lib.nv_capture_abort(self.handle)
-            self.context.capturing = False
-            self.context.captured = []
+            self._device.recording = None
             raise
-        graph = _vp()
-        code = self.lib.nv_capture_end(self.handle, ctypes.byref(graph))
-        self.context.capturing = False
-        buffers, self.context.captured = self.context.captured, []
-        _check(code)
-        if not graph.value:
-            raise BackendError("null graph", -1)
-        return Graph(self.context, graph.value, buffers)
+        exec_handle = _vp()
+        status = self.lib.nv_capture_end(self.handle, ctypes.byref(exec_handle))  # over whatever the status
+        held, self._device.recording = list(self._device.recording.values()), None
+        check_status(status, self.lib)
+        return Graph(self._device, exec_handle.value, held)
+
+    def _admit(self, op: str, args) -> None:
+        """Checks the tensor arguments of kernel `op` (the module's contract)."""
+        spans = []
+        for name, buf, width, dims, _ in args:
+            who = f"{op}: argument '{name}'"
+            if buf._memory.device is not self._device:
+                raise ArgumentError("foreign", f"{who} was not allocated by this Gpu")
+            need = byte_count(dims, width)
+            if need > buf._length:
+                raise ArgumentError("extent", f"{who} needs {need} bytes; its view holds {buf._length}")
+            if buf._offset % width:
+                raise ArgumentError("alignment", f"{who} starts at byte {buf._offset}, not a multiple of {width}")
+            spans.append((buf._memory, buf._offset, buf._offset + need))
+        for i, (name, _, _, _, written) in enumerate(args):
+            if not written:
+                continue
+            mem, lo, hi = spans[i]
+            for j, (other, olo, ohi) in enumerate(spans):
+                if j != i and other is mem and max(lo, olo) < min(hi, ohi):
+                    raise ArgumentError("overlap", f"{op}: written argument '{name}' shares bytes with "
+                                                   f"argument '{args[j][0]}'")
+        if self._device.recording is not None:
+            for _, buf, _, _, _ in args:
+                self._device.recording.setdefault(id(buf._memory), buf._memory)
+
+    def _call(self, status: int) -> None:
+        check_status(status, self.lib)
 
     # -------------------------------------------------------------- GEMM ---
     def gemm(self, x: Buffer, w: Buffer, y: Buffer, m: int, n: int, k: int) -> None:
-        self.tensor(x, [m, k], 2)
-        self.tensor(w, [n, k], 2)
-        self.tensor(y, [m, n], 2)
-        self.distinct(y, [x, w])
-        _check(self.lib.nv_gemm(self.handle, x.ptr, w.ptr, y.ptr, _dimension(m), _dimension(n), _dimension(k)))
+        """Y[m, n] = X[m, k] W[n, k]^T, bf16 in/out, fp32 accumulation."""
+        self._admit("gemm", [_r("x", x, 2, m, k), _r("w", w, 2, n, k), _w("y", y, 2, m, n)])
+        self._call(self.lib.nv_gemm(self.handle, x.ptr, w.ptr, y.ptr, m, n, k))
 
     # ----------------------------------------------------------- kernels ---
     def embedding(self, tokens: Buffer, weight: Buffer, out: Buffer, rows: int, hidden: int, vocab: int) -> None:
-        self.tensor(tokens, [rows], 4)
-        self.tensor(weight, [vocab, hidden], 2)
-        self.tensor(out, [rows, hidden], 2)
-        self.distinct(out, [tokens, weight])
-        _check(self.lib.nv_embedding(self.handle, tokens.ptr, weight.ptr, out.ptr, _dimension(rows),
-                                     _dimension(hidden), _dimension(vocab)))
+        self._admit("embedding", [_r("tokens", tokens, 4, rows), _r("weight", weight, 2, vocab, hidden),
+                                  _w("out", out, 2, rows, hidden)])
+        self._call(self.lib.nv_embedding(self.handle, tokens.ptr, weight.ptr, out.ptr, rows, hidden, vocab))
 
     def rms_norm(self, x: Buffer, weight: Buffer, out: Buffer, rows: int, hidden: int, eps: float) -> None:
-        _positive(eps, "RMS epsilon")
-        self.tensor(x, [rows, hidden], 2)
-        self.tensor(weight, [hidden], 2)
-        self.tensor(out, [rows, hidden], 2)
-        self.distinct(out, [x, weight])
-        _check(self.lib.nv_rms(self.handle, x.ptr, weight.ptr, out.ptr, _dimension(rows), _dimension(hidden), eps))
+        require_positive(eps, "rms_norm eps")
+        self._admit("rms_norm", [_r("x", x, 2, rows, hidden), _r("weight", weight, 2, hidden),
+                                 _w("out", out, 2, rows, hidden)])
+        self._call(self.lib.nv_rms(self.handle, x.ptr, weight.ptr, out.ptr, rows, hidden, eps))
 
     def add_rms_norm(self, x: Buffer, residual: Buffer, weight: Buffer, out: Buffer, rows: int, hidden: int,
                      eps: float) -> None:
-        """residual <- bf16(x + residual); out <- RMSNorm(f32(x) + f32(residual))."""
-        _positive(eps, "RMS epsilon")
-        self.tensor(x, [rows, hidden], 2)
-        self.tensor(residual, [rows, hidden], 2)
-        self.tensor(weight, [hidden], 2)
-        self.tensor(out, [rows, hidden], 2)
-        self.distinct(out, [x, residual, weight])
-        self.distinct(residual, [x, weight])
-        _check(self.lib.nv_add_rms(self.handle, x.ptr, residual.ptr, weight.ptr, out.ptr, _dimension(rows),
-                                   _dimension(hidden), eps))
+        """residual <- bf16(x + residual); out <- RMSNorm(f32(x) + f32(residual)) * weight."""
+        require_positive(eps, "add_rms_norm eps")
+        self._admit("add_rms_norm", [_r("x", x, 2, rows, hidden), _w("residual", residual, 2, rows, hidden),
+                                     _r("weight", weight, 2, hidden), _w("out", out, 2, rows, hidden)])
+        self._call(self.lib.nv_add_rms(self.handle, x.ptr, residual.ptr, weight.ptr, out.ptr, rows, hidden, eps))
 
     @staticmethod
-    def _heads(qheads: int, kvheads: int, head_dim: int) -> None:
-        _dimension(qheads)
-        _dimension(kvheads)
-        _dimension(head_dim)
-        if qheads % kvheads != 0:
-            raise ValueError("query heads must be a multiple of KV heads")
-        if head_dim % 2 != 0 or head_dim > 256:
-            raise ValueError("head dimension must be even and at most 256")
-        if qheads + kvheads > 65535:
-            raise ValueError("too many heads for one launch")
-
-    def _check_qkv_rope(self, qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows, qheads, kvheads,
-                        head_dim, block_size, num_blocks, eps) -> None:
-        self._heads(qheads, kvheads, head_dim)
-        _positive(eps, "RMS epsilon")
-        self.tensor(qkv, [rows, qheads + 2 * kvheads, head_dim], 2)
-        for w in (qweight, kweight):
-            self.tensor(w, [head_dim], 2)
-        for meta in (positions, slots):
-            self.tensor(meta, [rows], 4)
-        self.tensor(qout, [rows, qheads, head_dim], 2)
-        for cache in (kcache, vcache):
-            self.tensor(cache, [num_blocks, block_size, kvheads, head_dim], 2)
-        inputs = [qkv, qweight, kweight, positions, slots]
-        for out in (qout, kcache, vcache):
-            self.distinct(out, inputs)
-        self.distinct(qout, [kcache, vcache])
-        self.distinct(kcache, [vcache])
+    def _rope_args(qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows, qheads, kvheads, head_dim,
+                   block_size, num_blocks):
+        args = [_r("qkv", qkv, 2, rows, qheads + 2 * kvheads, head_dim), _r("qweight", qweight, 2, head_dim),
+                _r("kweight", kweight, 2, head_dim), _r("positions", positions, 4, rows), _r("slots", slots, 4, rows),
+                _w("kcache", kcache, 2, num_blocks, block_size, kvheads, head_dim),
+                _w("vcache", vcache, 2, num_blocks, block_size, kvheads, head_dim)]
+        if qout is not None:
+            args.append(_w("qout", qout, 2, rows, qheads, head_dim))
+        return args
 
     def qkv_rope(self, qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows, qheads, kvheads,
                  head_dim, block_size, num_blocks, eps, theta) -> None:
-        _positive(theta, "RoPE theta")
-        self._check_qkv_rope(qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows, qheads, kvheads,
-                             head_dim, block_size, num_blocks, eps)
-        _check(self.lib.nv_qkv_rope(self.handle, qkv.ptr, qweight.ptr, kweight.ptr, positions.ptr, slots.ptr,
-                                    qout.ptr, kcache.ptr, vcache.ptr, _dimension(rows), _dimension(qheads),
-                                    _dimension(kvheads), _dimension(head_dim), _dimension(block_size),
-                                    _dimension(num_blocks), eps, theta))
+        """Per-head q/k RMSNorm + NeoX RoPE (angle computed inline) + KV write."""
+        require_positive(eps, "qkv_rope eps")
+        require_positive(theta, "qkv_rope theta")
+        require_head_layout(qheads, kvheads, head_dim)
+        self._admit("qkv_rope", self._rope_args(qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows,
+                                                qheads, kvheads, head_dim, block_size, num_blocks))
+        self._call(self.lib.nv_qkv_rope(self.handle, qkv.ptr, qweight.ptr, kweight.ptr, positions.ptr, slots.ptr,
+                                        qout.ptr, kcache.ptr, vcache.ptr, rows, qheads, kvheads, head_dim, block_size,
+                                        num_blocks, eps, theta))
 
     def rope_cache(self, cache: Buffer, max_positions: int, head_dim: int, theta: float) -> None:
-        """fp32 [positions, cos(head_dim/2) | sin(head_dim/2)], built once at load time."""
-        self._heads(1, 1, head_dim)
-        _positive(theta, "RoPE theta")
-        self.tensor(cache, [max_positions, head_dim], 4)
-        _check(self.lib.nv_rope_cache(self.handle, cache.ptr, _dimension(max_positions), _dimension(head_dim),
-                                      theta))
+        """f32 [max_positions, head_dim]: cos of the head_dim/2 pairs, then sin."""
+        require_positive(theta, "rope_cache theta")
+        require_head_layout(1, 1, head_dim)
+        self._admit("rope_cache", [_w("cache", cache, 4, max_positions, head_dim)])
+        self._call(self.lib.nv_rope_cache(self.handle, cache.ptr, max_positions, head_dim, theta))
 
     def qkv_rope_cached(self, qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows, qheads, kvheads,
                         head_dim, block_size, num_blocks, eps, rope_cache, max_positions) -> None:
-        self._check_qkv_rope(qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows, qheads, kvheads,
-                             head_dim, block_size, num_blocks, eps)
-        self.tensor(rope_cache, [max_positions, head_dim], 4)
-        for output in (qout, kcache, vcache):
-            self.distinct(output, [rope_cache])
-        _check(self.lib.nv_qkv_rope_cached(self.handle, qkv.ptr, qweight.ptr, kweight.ptr, positions.ptr,
-                                           slots.ptr, qout.ptr, kcache.ptr, vcache.ptr, _dimension(rows),
-                                           _dimension(qheads), _dimension(kvheads), _dimension(head_dim),
-                                           _dimension(block_size), _dimension(num_blocks), eps, rope_cache.ptr,
-                                           _dimension(max_positions)))
+        """As qkv_rope with cos/sin from the table; positions outside [0, max_positions) rotate by 0."""
+        require_positive(eps, "qkv_rope_cached eps")
+        require_head_layout(qheads, kvheads, head_dim)
+        args = self._rope_args(qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows, qheads, kvheads,
+                               head_dim, block_size, num_blocks)
+        self._admit("qkv_rope_cached", args + [_r("rope_cache", rope_cache, 4, max_positions, head_dim)])
+        self._call(self.lib.nv_qkv_rope_cached(self.handle, qkv.ptr, qweight.ptr, kweight.ptr, positions.ptr,
+                                               slots.ptr, qout.ptr, kcache.ptr, vcache.ptr, rows, qheads, kvheads,
+                                               head_dim, block_size, num_blocks, eps, rope_cache.ptr, max_positions))
+
+    @staticmethod
+    def _context_limit(max_context: int) -> None:
+        if not 1 <= max_context <= 4096:
+            raise ArgumentError("value", f"max_context {max_context} outside [1, 4096]")
 
     def paged_attention(self, q: Buffer, kcache: Buffer, vcache: Buffer, positions: Buffer, seq_indices: Buffer,
                         block_tables: Buffer, out: Buffer, rows: int, qheads: int, kvheads: int, head_dim: int,
                         block_size: int, num_blocks: int, table_stride: int, batch_size: int,
                         max_context: int) -> None:
-        """Causal paged GQA over flattened ragged prefill and decode rows
-        (src/gpu.rs:826-887). KV layout [blocks, block_size, kvheads, head_dim];
-        each row attends to positions[row] + 1 keys of sequence seq_indices[row]."""
-        self._heads(qheads, kvheads, head_dim)
-        if not 0 < max_context <= 4096:
-            raise ValueError("paged attention supports at most 4096 context tokens")
-        self.tensor(q, [rows, qheads, head_dim], 2)
-        self.tensor(out, [rows, qheads, head_dim], 2)
-        for cache in (kcache, vcache):
-            self.tensor(cache, [num_blocks, block_size, kvheads, head_dim], 2)
-        for meta in (positions, seq_indices):
-            self.tensor(meta, [rows], 4)
-        self.tensor(block_tables, [batch_size, table_stride], 4)
-        self.distinct(out, [q, kcache, vcache, positions, seq_indices, block_tables])
-        _check(self.lib.nv_attention(self.handle, q.ptr, kcache.ptr, vcache.ptr, positions.ptr, seq_indices.ptr,
-                                     block_tables.ptr, out.ptr, _dimension(rows), _dimension(qheads),
-                                     _dimension(kvheads), _dimension(head_dim), _dimension(block_size),
-                                     _dimension(num_blocks), _dimension(table_stride), _dimension(batch_size),
-                                     _dimension(max_context)))
+        """Causal paged GQA over flattened ragged rows; row r reads positions[r] + 1 keys."""
+        require_head_layout(qheads, kvheads, head_dim)
+        self._context_limit(max_context)
+        self._admit("paged_attention", [
+            _r("q", q, 2, rows, qheads, head_dim), _r("kcache", kcache, 2, num_blocks, block_size, kvheads, head_dim),
+            _r("vcache", vcache, 2, num_blocks, block_size, kvheads, head_dim), _r("positions", positions, 4, rows),
+            _r("seq_indices", seq_indices, 4, rows), _r("block_tables", block_tables, 4, batch_size, table_stride),
+            _w("out", out, 2, rows, qheads, head_dim)])
+        self._call(self.lib.nv_attention(self.handle, q.ptr, kcache.ptr, vcache.ptr, positions.ptr, seq_indices.ptr,
+                                         block_tables.ptr, out.ptr, rows, qheads, kvheads, head_dim, block_size,
+                                         num_blocks, table_stride, batch_size, max_context))
 
     def attention_qkv_rope(self, qkv: Buffer, qweight: Buffer, kweight: Buffer, positions: Buffer, slots: Buffer,
                            kcache: Buffer, vcache: Buffer, seq_indices: Buffer, block_tables: Buffer, out: Buffer,
                            rows: int, qheads: int, kvheads: int, head_dim: int, block_size: int, num_blocks: int,
                            table_stride: int, batch_size: int, max_context: int, eps: float, rope_cache: Buffer,
                            max_positions: int) -> None:
-        """qkv_rope_cached followed by paged_attention in one launch (head dim
-        128), for decode batches: no row may read a KV slot that another row
-        writes. The rotated q is not written to memory."""
+        """qkv_rope_cached + paged_attention in one launch for decode batches (head dim 128);
+        no row may read a KV slot that another row writes."""
+        require_positive(eps, "attention_qkv_rope eps")
+        require_head_layout(qheads, kvheads, head_dim)
         if head_dim != 128:
-            raise ValueError("fused attention needs head_dim 128")
-        if not 0 < max_context <= 4096:
-            raise ValueError("paged attention supports at most 4096 context tokens")
-        self.tensor(out, [rows, qheads, head_dim], 2)
-        self.tensor(seq_indices, [rows], 4)
-        self.tensor(block_tables, [batch_size, table_stride], 4)
-        self.tensor(rope_cache, [max_positions, head_dim], 4)
-        self._check_qkv_rope(qkv, qweight, kweight, positions, slots, out, kcache, vcache, rows, qheads, kvheads,
-                             head_dim, block_size, num_blocks, eps)
-        self.distinct(out, [qkv, kcache, vcache, positions, seq_indices, block_tables, rope_cache])
-        for cache in (kcache, vcache):
-            self.distinct(cache, [rope_cache, seq_indices, block_tables])
-        _check(self.lib.nv_attention_qkv_rope(self.handle, qkv.ptr, qweight.ptr, kweight.ptr, positions.ptr,
-                                              slots.ptr, kcache.ptr, vcache.ptr, seq_indices.ptr, block_tables.ptr,
-                                              out.ptr, _dimension(rows), _dimension(qheads), _dimension(kvheads),
-                                              _dimension(head_dim), _dimension(block_size), _dimension(num_blocks),
-                                              _dimension(table_stride), _dimension(batch_size),
-                                              _dimension(max_context), eps, rope_cache.ptr,
-                                              _dimension(max_positions)))
+            raise ArgumentError("value", "attention_qkv_rope takes head_dim 128 only")
+        self._context_limit(max_context)
+        args = self._rope_args(qkv, qweight, kweight, positions, slots, None, kcache, vcache, rows, qheads, kvheads,
+                               head_dim, block_size, num_blocks)
+        self._admit("attention_qkv_rope", args + [
+            _r("seq_indices", seq_indices, 4, rows), _r("block_tables", block_tables, 4, batch_size, table_stride),
+            _r("rope_cache", rope_cache, 4, max_positions, head_dim), _w("out", out, 2, rows, qheads, head_dim)])
+        self._call(self.lib.nv_attention_qkv_rope(self.handle, qkv.ptr, qweight.ptr, kweight.ptr, positions.ptr,
+                                                  slots.ptr, kcache.ptr, vcache.ptr, seq_indices.ptr,
+                                                  block_tables.ptr, out.ptr, rows, qheads, kvheads, head_dim,
+                                                  block_size, num_blocks, table_stride, batch_size, max_context, eps,
+                                                  rope_cache.ptr, max_positions))
 
     def kv_write(self, k: Buffer, v: Buffer, slots: Buffer, kcache: Buffer, vcache: Buffer, rows: int,
                  kvheads: int, head_dim: int, block_size: int, num_blocks: int) -> None:
-        """Standalone paged KV-cache slot write (no counterpart method in src/gpu.rs)."""
-        for t in (k, v):
-            self.tensor(t, [rows, kvheads, head_dim], 2)
-        self.tensor(slots, [rows], 4)
-        for cache in (kcache, vcache):
-            self.tensor(cache, [num_blocks, block_size, kvheads, head_dim], 2)
-        for out in (kcache, vcache):
-            self.distinct(out, [k, v, slots])
-        self.distinct(kcache, [vcache])
-        _check(self.lib.nv_kv_write(self.handle, k.ptr, v.ptr, slots.ptr, kcache.ptr, vcache.ptr, _dimension(rows),
-                                    _dimension(kvheads), _dimension(head_dim), _dimension(block_size),
-                                    _dimension(num_blocks)))
+        """kcache[slots[r]] = k[r], vcache[slots[r]] = v[r] for slots in [0, block_size * num_blocks)."""
+        if as_dim(kvheads) * as_dim(head_dim) > INT_MAX:
+            raise ArgumentError("dimension", "kv_write: kvheads * head_dim exceeds 2^31 - 1")
+        self._admit("kv_write", [
+            _r("k", k, 2, rows, kvheads, head_dim), _r("v", v, 2, rows, kvheads, head_dim),
+            _r("slots", slots, 4, rows), _w("kcache", kcache, 2, num_blocks, block_size, kvheads, head_dim),
+            _w("vcache", vcache, 2, num_blocks, block_size, kvheads, head_dim)])
+        self._call(self.lib.nv_kv_write(self.handle, k.ptr, v.ptr, slots.ptr, kcache.ptr, vcache.ptr, rows, kvheads,
+                                        head_dim, block_size, num_blocks))
 
     def silu_mul(self, gateup: Buffer, out: Buffer, rows: int, intermediate: int) -> None:
-        self.tensor(gateup, [rows, 2, intermediate], 2)
-        self.tensor(out, [rows, intermediate], 2)
-        if intermediate > 0x7FFFFFFF // 2:
-            raise ValueError("intermediate size too large")
-        self.distinct(out, [gateup])
-        _check(self.lib.nv_silu(self.handle, gateup.ptr, out.ptr, _dimension(rows), _dimension(intermediate)))
+        """out[r] = bf16(silu(gate) * up) with gateup = [rows, 2, intermediate]."""
+        if intermediate > INT_MAX // 2:
+            raise ArgumentError("dimension", "silu_mul: 2 * intermediate exceeds 2^31 - 1")
+        self._admit("silu_mul", [_r("gateup", gateup, 2, rows, 2, intermediate),
+                                 _w("out", out, 2, rows, intermediate)])
+        self._call(self.lib.nv_silu(self.handle, gateup.ptr, out.ptr, rows, intermediate))
 
     def gather(self, x: Buffer, indices: Buffer, out: Buffer, rows: int, hidden: int, input_rows: int) -> None:
-        self.tensor(x, [input_rows, hidden], 2)
-        self.tensor(indices, [rows], 4)
-        self.tensor(out, [rows, hidden], 2)
-        self.distinct(out, [x, indices])
-        _check(self.lib.nv_gather(self.handle, x.ptr, indices.ptr, out.ptr, _dimension(rows), _dimension(hidden),
-                                  _dimension(input_rows)))
+        self._admit("gather", [_r("x", x, 2, input_rows, hidden), _r("indices", indices, 4, rows),
+                               _w("out", out, 2, rows, hidden)])
+        self._call(self.lib.nv_gather(self.handle, x.ptr, indices.ptr, out.ptr, rows, hidden, input_rows))
+
+    @staticmethod
+    def _sampler_args(logits, temperatures, seeds, out, batch, vocab):
+        return [_r("logits", logits, 2, batch, vocab), _r("temperatures", temperatures, 4, batch),
+                _r("seeds", seeds, 8, batch), _w("out", out, 4, batch)]
 
     def sample(self, logits: Buffer, temperatures: Buffer, seeds: Buffer, out: Buffer, batch: int,
                vocab: int) -> None:
         """bf16 logits; f32 temperatures (<= 0 greedy); u64 seeds; i32 output."""
-        self.tensor(logits, [batch, vocab], 2)
-        self.tensor(temperatures, [batch], 4)
-        self.tensor(seeds, [batch], 8)
-        self.tensor(out, [batch], 4)
-        self.distinct(out, [logits, temperatures, seeds])
-        _check(self.lib.nv_sample(self.handle, logits.ptr, temperatures.ptr, seeds.ptr, out.ptr, _dimension(batch),
-                                  _dimension(vocab)))
+        self._admit("sample", self._sampler_args(logits, temperatures, seeds, out, batch, vocab))
+        self._call(self.lib.nv_sample(self.handle, logits.ptr, temperatures.ptr, seeds.ptr, out.ptr, batch, vocab))
 
     def sample_parallel(self, logits: Buffer, temperatures: Buffer, seeds: Buffer, out: Buffer,
                         partial_scores: Buffer, partial_ids: Buffer, batch: int, vocab: int) -> None:
-        """Two-stage vocabulary reduction; scratch holds batch x ceil(vocab/2048) entries."""
-        self.tensor(logits, [batch, vocab], 2)
-        self.tensor(temperatures, [batch], 4)
-        self.tensor(seeds, [batch], 8)
-        self.tensor(out, [batch], 4)
+        """Vocabulary-parallel sampling; scratch holds batch x ceil(vocab/2048) entries."""
         parts = -(-vocab // 2048)
-        self.tensor(partial_scores, [batch, parts], 4)
-        self.tensor(partial_ids, [batch, parts], 4)
-        for output in (out, partial_scores, partial_ids):
-            self.distinct(output, [logits, temperatures, seeds])
-        self.distinct(out, [partial_scores, partial_ids])
-        self.distinct(partial_scores, [partial_ids])
-        _check(self.lib.nv_sample_parallel(self.handle, logits.ptr, temperatures.ptr, seeds.ptr, out.ptr,
-                                           partial_scores.ptr, partial_ids.ptr, _dimension(batch),
-                                           _dimension(vocab)))
-
+        self._admit("sample_parallel", self._sampler_args(logits, temperatures, seeds, out, batch, vocab) + [
+            _w("partial_scores", partial_scores, 4, batch, parts), _w("partial_ids", partial_ids, 4, batch, parts)])
+        self._call(self.lib.nv_sample_parallel(self.handle, logits.ptr, temperatures.ptr, seeds.ptr, out.ptr,
+                                               partial_scores.ptr, partial_ids.ptr, batch, vocab))
 
     STATIC_PARTIALS = 1 << 17
 
@@ -559,13 +533,9 @@ class Gpu:
                                vocab: int) -> None:
         """sample_parallel with the library's static partials instead of caller
         scratch (no allocation): batch * ceil(vocab / 2048) <= 131072."""
-        self.tensor(logits, [batch, vocab], 2)
-        self.tensor(temperatures, [batch], 4)
-        self.tensor(seeds, [batch], 8)
-        self.tensor(out, [batch], 4)
-        self.distinct(out, [logits, temperatures, seeds])
-        _check(self.lib.nv_sample_parallel_static(self.handle, logits.ptr, temperatures.ptr, seeds.ptr, out.ptr,
-                                                  _dimension(batch), _dimension(vocab)))
+        self._admit("sample_parallel_static", self._sampler_args(logits, temperatures, seeds, out, batch, vocab))
+        self._call(self.lib.nv_sample_parallel_static(self.handle, logits.ptr, temperatures.ptr, seeds.ptr, out.ptr,
+                                                      batch, vocab))
 
 
 def bf16_bits(values) -> np.ndarray:

@@ -49,6 +49,22 @@ struct Failure {
         if (!thrown_) throw harness::Failure{std::string(__FILE__ ":") + std::to_string(__LINE__) + ": no throw: " #expr}; \
     } while (0)
 
+// Throws unless `expr` throws nvr::Error of the given Fault kind.
+#define CHECK_FAULT(expr, kind)                                                                             \
+    do {                                                                                                    \
+        bool thrown_ = false;                                                                               \
+        try {                                                                                               \
+            expr;                                                                                           \
+        } catch (const nvr::Error& e_) {                                                                    \
+            if (e_.fault() != (kind))                                                                       \
+                throw harness::Failure{std::string(__FILE__ ":") + std::to_string(__LINE__) + ": fault " +   \
+                                       nvr::fault_name(e_.fault()) + " (" + e_.what() + "), expected " +   \
+                                       nvr::fault_name(kind)};                                              \
+            thrown_ = true;                                                                                 \
+        }                                                                                                   \
+        if (!thrown_) throw harness::Failure{std::string(__FILE__ ":") + std::to_string(__LINE__) + ": no throw: " #expr}; \
+    } while (0)
+
 }  // namespace harness
 
 int main(int argc, char** argv) {

@@ -1,6 +1,6 @@
 // The reference's own GPU tests (src/gpu.rs:1148-1472 of nano-vllm-rs),
-// restated over the C++ host API (nano-vllm-rs_amd/host/gpu.hpp), plus
-// CPU-only checks of its argument validation.
+// restated over the C++ host API (nano-vllm-rs_amd/host/gpu.hpp), plus checks
+// of that API's argument contract (each rejection by its Fault kind).
 //
 // Usage: test_gpu_host cpu|gpu   -> runs that suite, exit status 0 when all pass.
 #include <cmath>
@@ -42,38 +42,30 @@ std::vector<float> values(const nvr::Buffer& buffer, std::size_t count) {
 }
 
 // -------------------------------------------------------------- CPU suite --
-TEST(dimension_extent_and_positive_checks, "cpu") {
-    CHECK(nvr::dimension(1) == 1);
-    CHECK(nvr::dimension(0x7fffffff) == 0x7fffffff);
-    CHECK_THROWS(nvr::dimension(0));
-    CHECK_THROWS(nvr::dimension(std::size_t(0x80000000u)));
-    CHECK(nvr::extent({3, 5}, 2) == 30);
-    CHECK_THROWS(nvr::extent({3, 0}, 2));
-    CHECK_THROWS(nvr::extent({0x7fffffff, 0x7fffffff, 0x7fffffff}, 8));  // byte count overflow
-    nvr::positive(1e-6f, "eps");
-    CHECK_THROWS(nvr::positive(0.0f, "eps"));
-    CHECK_THROWS(nvr::positive(-1.0f, "eps"));
-    CHECK_THROWS(nvr::positive(INFINITY, "eps"));
-    CHECK_THROWS(nvr::positive(NAN, "eps"));
-    try {
-        nvr::positive(0.0f, "RMS epsilon");
-    } catch (const nvr::Error& e) {
-        CHECK(std::string(e.what()) == "RMS epsilon must be positive and finite");
-    }
+TEST(dimension_byte_count_and_scalar_checks, "cpu") {
+    CHECK(nvr::as_dim(1) == 1);
+    CHECK(nvr::as_dim(0x7fffffff) == 0x7fffffff);
+    CHECK_FAULT(nvr::as_dim(0), nvr::Fault::Dimension);
+    CHECK_FAULT(nvr::as_dim(std::size_t(0x80000000u)), nvr::Fault::Dimension);
+    CHECK(nvr::byte_count({3, 5}, 2) == 30);
+    CHECK_FAULT(nvr::byte_count({3, 0}, 2), nvr::Fault::Dimension);
+    CHECK_FAULT(nvr::byte_count({0x7fffffff, 0x7fffffff, 0x7fffffff}, 8), nvr::Fault::Extent);
+    nvr::require_positive(1e-6f, "eps");
+    for (float bad : {0.0f, -1.0f, INFINITY, NAN}) CHECK_FAULT(nvr::require_positive(bad, "eps"), nvr::Fault::Value);
 }
 
-TEST(head_shape_checks, "cpu") {  // src/gpu.rs:643-660
-    nvr::heads(16, 8, 128);
-    nvr::heads(1, 1, 256);
-    CHECK_THROWS(nvr::heads(16, 6, 128));     // not a multiple
-    CHECK_THROWS(nvr::heads(16, 8, 127));     // odd
-    CHECK_THROWS(nvr::heads(16, 8, 258));     // above 256
-    CHECK_THROWS(nvr::heads(65535, 1, 128));  // qheads + kvheads > 65535
-    CHECK_THROWS(nvr::heads(0, 1, 128));
+TEST(head_layout_checks, "cpu") {
+    nvr::require_head_layout(16, 8, 128);
+    nvr::require_head_layout(1, 1, 256);
+    CHECK_FAULT(nvr::require_head_layout(16, 6, 128), nvr::Fault::Value);     // not a whole number of groups
+    CHECK_FAULT(nvr::require_head_layout(16, 8, 127), nvr::Fault::Value);     // odd
+    CHECK_FAULT(nvr::require_head_layout(16, 8, 258), nvr::Fault::Value);     // above 256
+    CHECK_FAULT(nvr::require_head_layout(65535, 1, 128), nvr::Fault::Value);  // q + KV heads above 65535
+    CHECK_FAULT(nvr::require_head_layout(0, 1, 128), nvr::Fault::Dimension);
 }
 
 TEST(device_index_and_seed, "cpu") {
-    CHECK_THROWS(nvr::Gpu(-1));
+    CHECK_FAULT(nvr::Gpu(-1), nvr::Fault::Value);
     // src/runtime.rs:780-790: mix(mix(base) ^ mix(request) ^ mix(generated)),
     // mix = SplitMix64. With all zeros it is mix(mix(0)), mix(0) being the
     // published 0xe220a8397b1dcdaf; request and generated commute.
@@ -88,15 +80,25 @@ TEST(gpu_views_keep_allocations_and_reject_overlap, "gpu") {  // src/gpu.rs:1169
     packed.upload_i32({1, 3, 0, 0, 5, 6, 7, 8});
     nvr::Buffer tokens = packed.slice(0, 8);
     nvr::Buffer adjacent = packed.slice(8, 8);
-    nvr::Gpu::distinct(tokens, {&adjacent});
+    CHECK(!tokens.overlaps(adjacent));
     const nvr::Buffer straddling = packed.slice(4, 8);
-    CHECK_THROWS(nvr::Gpu::distinct(tokens, {&straddling}));
-    CHECK_THROWS(tokens.slice(4, 8));
-    CHECK_THROWS(packed.slice(SIZE_MAX, 1));
-    CHECK_THROWS(gpu.tensor(packed.slice(1, 8), {1}, 4));
+    CHECK(tokens.overlaps(straddling));
+    CHECK_FAULT(tokens.slice(4, 8), nvr::Fault::Extent);  // past the end of the view
+    CHECK_FAULT(packed.slice(SIZE_MAX, 1), nvr::Fault::Extent);
     nvr::Buffer weights = gpu.alloc(8);
     weights.upload_bytes(bf16({1, 2, 3, 4}));
     nvr::Buffer out = gpu.alloc(4);
+    // A misaligned i32 view, an output sharing bytes with an input, a view
+    // too small for its shape, and a buffer of another context.
+    CHECK_FAULT(gpu.embedding(packed.slice(1, 8), weights, out, 2, 1, 4), nvr::Fault::Alignment);
+    CHECK_FAULT(gpu.embedding(tokens, weights, weights.slice(0, 4), 2, 1, 4), nvr::Fault::Overlap);
+    CHECK_FAULT(gpu.embedding(tokens, weights, out, 3, 1, 4), nvr::Fault::Extent);
+    nvr::Gpu other(0);
+    nvr::Buffer foreign = other.alloc(4);
+    CHECK_FAULT(gpu.embedding(tokens, weights, foreign, 2, 1, 4), nvr::Fault::Foreign);
+    // Adjacent views of one allocation are separate arguments.
+    gpu.embedding(tokens, weights, packed.slice(16, 4), 2, 1, 4);
+    CHECK((values(packed.slice(16, 4), 2) == std::vector<float>{2, 4}));
     nvr::Graph graph = gpu.capture([&] { gpu.embedding(tokens, weights, out, 2, 1, 4); });
     {  // the graph keeps the views' allocation alive
         nvr::Buffer gone = std::move(tokens), also = std::move(adjacent), last = std::move(packed);
@@ -159,8 +161,8 @@ TEST(gpu_gemm_rms_sampling_graph, "gpu") {  // src/gpu.rs:1290-1330
     w.upload_bytes(bf16({1, 0, 1, 0, 1, 0}));
     gpu.gemm(x, w, y, 2, 2, 3);
     CHECK((values(y, 4) == std::vector<float>{4, 2, 10, 5}));
-    CHECK_THROWS(gpu.gemm(x, w, y, 3, 2, 3));
-    CHECK_THROWS(gpu.gemm(x, w, x, 2, 2, 3));
+    CHECK_FAULT(gpu.gemm(x, w, y, 3, 2, 3), nvr::Fault::Extent);
+    CHECK_FAULT(gpu.gemm(x, w, x, 2, 2, 3), nvr::Fault::Overlap);
     nvr::Buffer normw = gpu.alloc(4), normalized = gpu.alloc(8);
     normw.upload_bytes(bf16({1, 1}));
     gpu.rms_norm(y, normw, normalized, 2, 2, 1e-6f);
@@ -180,7 +182,8 @@ TEST(gpu_gemm_rms_sampling_graph, "gpu") {  // src/gpu.rs:1290-1330
     }
     graph.replay();
     gpu.sync();
-    CHECK_THROWS(gpu.capture([&] { gpu.alloc(4); }));
+    // The library refuses allocation during a capture; the capture is abandoned.
+    CHECK_FAULT(gpu.capture([&] { gpu.alloc(4); }), nvr::Fault::Backend);
     gpu.sync();  // the failed capture left the context usable
 }
 
@@ -277,7 +280,7 @@ TEST(gpu_ragged_gqa_matches_cpu, "gpu") {
 TEST(gpu_capture_failure_leaves_the_context_usable, "gpu") {
     nvr::Gpu gpu(0);
     nvr::Buffer a = gpu.alloc(64), b = gpu.alloc(64);
-    CHECK_THROWS(gpu.capture([&] { gpu.silu_mul(a, a, 1, 16); }));  // output aliases the input
+    CHECK_FAULT(gpu.capture([&] { gpu.silu_mul(a, a, 1, 16); }), nvr::Fault::Overlap);
     gpu.sync();
     nvr::Graph graph = gpu.capture([&] { gpu.silu_mul(a, b, 1, 16); });
     graph.replay();

@@ -3,8 +3,9 @@
 - libnano_hip.so loads and exports every function include/nano_hip.h declares,
   and the host wrapper (nvr.py) declares a signature for each of them;
 - host-only entry points (nv_sampling_seed, nv_last_error) work without a GPU;
-- the wrapper's validation (extents, alignment, aliasing, capture rules)
-  mirrors src/gpu.rs:222-509 and rejects what the reference rejects.
+- the wrapper's argument contract (dimensions, extents, alignment, buffer
+  ownership, overlapping outputs, scalars, head layouts), each rejection by
+  the rule it breaks.
 """
 import os
 import re
@@ -67,85 +68,67 @@ def test_library_has_no_oracle_dependency():
 
 
 # -------------------------------------------------- host-side validation ----
-class _FakeContext:
-    def __init__(self):
-        self.capturing = False
-        self.captured = []
-
-    def outside_capture(self):
-        if self.capturing:
-            raise ValueError("allocation, transfer and synchronization are forbidden during graph capture")
-
-
 def _fake_gpu():
+    """A Gpu with no device behind it: argument admission only (no kernel runs)."""
     g = object.__new__(nvr.Gpu)
-    g.context = _FakeContext()
+    g._device = nvr._Device(None, 0)
     g.lib = None
     return g
 
 
-def _fake_buffer(ctx, nbytes, ptr=0x10000):
-    alloc = object.__new__(nvr._Allocation)
-    alloc.context, alloc.ptr, alloc.bytes = ctx, None, nbytes  # ptr None: __del__ frees nothing
-    alloc.ptr_value = ptr
-    return nvr.Buffer(alloc, 0, nbytes)
+def _fake_buffer(gpu, nbytes):
+    return nvr.Buffer(nvr._Memory(gpu._device, None, nbytes), 0, nbytes)  # address None: nothing is freed
 
 
-def test_views_alignment_and_aliasing_rules():
-    """Host half of src/gpu.rs:1169-1192."""
+def _fault(fault, fn, *args):
+    with pytest.raises(nvr.ArgumentError) as e:
+        fn(*args)
+    assert e.value.fault == fault, str(e.value)
+
+
+def test_views_and_argument_admission():
     gpu = _fake_gpu()
-    packed = _fake_buffer(gpu.context, 32)
-    tokens = packed.slice(0, 8)
-    adjacent = packed.slice(8, 8)
-    nvr.Gpu.distinct(tokens, [adjacent])  # adjacent views do not overlap
-    with pytest.raises(ValueError):
-        nvr.Gpu.distinct(tokens, [packed.slice(4, 8)])
-    with pytest.raises(ValueError):
-        tokens.slice(4, 8)  # past the end of the view
-    with pytest.raises(ValueError):
-        packed.slice(2**64 - 1, 1)
-    with pytest.raises(ValueError):
-        gpu.tensor(packed.slice(1, 8), [1], 4)  # misaligned i32 view
-    gpu.tensor(packed.slice(4, 8), [2], 4)
-    with pytest.raises(ValueError):
-        gpu.tensor(packed, [0], 4)  # zero dimension
-    with pytest.raises(ValueError):
-        gpu.tensor(packed, [9], 4)  # extent beyond the buffer
-    other = _fake_buffer(_FakeContext(), 32)
-    with pytest.raises(ValueError):
-        gpu.tensor(other, [1], 4)  # different context
+    packed = _fake_buffer(gpu, 32)
+    tokens, adjacent, straddling = packed.slice(0, 8), packed.slice(8, 8), packed.slice(4, 8)
+    assert not tokens.overlaps(adjacent) and tokens.overlaps(straddling)
+    _fault("extent", tokens.slice, 4, 8)  # past the end of the view
+    _fault("extent", packed.slice, 2**64 - 1, 1)
+    weights, out = _fake_buffer(gpu, 8), _fake_buffer(gpu, 4)
+    _fault("alignment", gpu.embedding, packed.slice(1, 8), weights, out, 2, 1, 4)
+    _fault("overlap", gpu.embedding, tokens, weights, weights.slice(0, 4), 2, 1, 4)
+    _fault("extent", gpu.embedding, tokens, weights, out, 3, 1, 4)
+    _fault("dimension", gpu.embedding, tokens, weights, out, 0, 1, 4)
+    _fault("dimension", gpu.embedding, tokens, weights, out, 2**31, 1, 4)
+    _fault("foreign", gpu.embedding, tokens, weights, _fake_buffer(_fake_gpu(), 4), 2, 1, 4)
+    # Only the bytes an argument covers count: a written view that shares the
+    # allocation, but not the bytes, of an input is accepted up to the C call.
+    with pytest.raises(AttributeError):  # the fake Gpu has no library to call
+        gpu.embedding(tokens, weights, packed.slice(16, 4), 2, 1, 4)
 
 
-def test_kernel_wrappers_reject_bad_arguments_before_calling():
+def test_kernel_wrappers_reject_bad_scalars_and_layouts():
     gpu = _fake_gpu()
-    ctx = gpu.context
-    x = _fake_buffer(ctx, 8 * 1024 * 2)
-    w = _fake_buffer(ctx, 1024 * 2)
-    with pytest.raises(ValueError):
-        gpu.rms_norm(x, w, x, 8, 1024, 1e-6)  # out aliases x
-    out = _fake_buffer(ctx, 8 * 1024 * 2)
+    x, w, out = _fake_buffer(gpu, 8 * 1024 * 2), _fake_buffer(gpu, 1024 * 2), _fake_buffer(gpu, 8 * 1024 * 2)
     for eps in (0.0, -1.0, float("nan"), float("inf")):
-        with pytest.raises(ValueError):
-            gpu.rms_norm(x, w, out, 8, 1024, eps)
-    with pytest.raises(ValueError):
-        gpu.rms_norm(x, w, out, 9, 1024, 1e-6)  # x too small for 9 rows
-    with pytest.raises(ValueError):
-        nvr.Gpu._heads(16, 3, 128)  # qh % kvh != 0
-    with pytest.raises(ValueError):
-        nvr.Gpu._heads(16, 8, 129)  # odd head dim
-    with pytest.raises(ValueError):
-        nvr.Gpu._heads(16, 8, 258)
-    logits = _fake_buffer(ctx, 2 * 151936 * 2)
-    small = _fake_buffer(ctx, 16)
-    with pytest.raises(ValueError):  # scratch needs batch * ceil(vocab / 2048) entries
-        gpu.sample_parallel(logits, small, small, _fake_buffer(ctx, 8), small, small, 2, 151936)
+        _fault("value", gpu.rms_norm, x, w, out, 8, 1024, eps)
+    _fault("overlap", gpu.rms_norm, x, w, x, 8, 1024, 1e-6)  # out is x
+    _fault("value", nvr.require_head_layout, 16, 3, 128)  # q heads do not group over KV heads
+    _fault("value", nvr.require_head_layout, 16, 8, 129)  # odd head dim
+    _fault("value", nvr.require_head_layout, 16, 8, 258)  # above 256
+    _fault("value", nvr.require_head_layout, 65535, 1, 128)
+    logits = _fake_buffer(gpu, 2 * 151936 * 2)
+    small = _fake_buffer(gpu, 16)
+    # scratch needs batch * ceil(vocab / 2048) entries
+    _fault("extent", gpu.sample_parallel, logits, small, small.slice(0, 16), _fake_buffer(gpu, 8), _fake_buffer(gpu, 16),
+           _fake_buffer(gpu, 16), 2, 151936)
+    kc = _fake_buffer(gpu, 1 << 20)
+    _fault("value", gpu.paged_attention, x, kc, kc, small, small, small, out, 1, 16, 8, 128, 16, 1, 1, 1, 5000)
 
 
-def test_capture_forbids_transfers():
-    ctx = _FakeContext()
-    ctx.capturing = True
-    with pytest.raises(ValueError):
-        ctx.outside_capture()
+def test_capture_state_is_tracked_per_gpu():
+    gpu = _fake_gpu()
+    gpu._device.recording = {}
+    _fault("value", gpu.capture, lambda: None)  # a capture inside a capture
 
 
 def test_bf16_helpers_round_trip():

@@ -1,12 +1,13 @@
 """The C++ host side through its test binaries:
 
-- tests/cpp/test_gpu_host: the host API (nano-vllm-rs_amd/host/gpu.hpp, the
-  mirror of src/gpu.rs): argument checks on the CPU, and the reference's own
-  GPU tests (src/gpu.rs:1148-1472) restated in C++ on a GPU;
-- tests/cpp/test_model: the Qwen3 runner (host/model.hpp, the mirror of
-  src/model.rs): the packed-metadata test of src/model.rs:1232-1297 and config
-  checks on the CPU; batch validation, graph replay against the eager forward
-  and decode against prefill on a GPU."""
+- tests/cpp/test_gpu_host: the host API (nano-vllm-rs_amd/host/gpu.hpp):
+  its argument contract on the CPU, and the reference's own GPU tests
+  (src/gpu.rs:1148-1472) restated in C++ on a GPU;
+- tests/cpp/test_model: the Qwen3 runner (host/model.hpp): the step record and
+  config checks on the CPU; on a GPU the batch contract, the fused-attention
+  choice, the forward against the CPU oracle stage by stage, fused against
+  split attention, graph replay against the eager forward and decode against
+  prefill."""
 import os
 import subprocess
 
@@ -32,7 +33,7 @@ def test_cpp_host_argument_checks():
 def test_cpp_model_metadata_and_config():
     out = _run("test_model", "cpu")
     assert "FAILED" not in out
-    assert "packed_metadata_preserves_values_alignment_and_clears_table_padding ... ok" in out
+    assert "step_record_layout_fill_and_table_padding ... ok" in out
 
 
 @pytest.mark.gpu
@@ -49,7 +50,8 @@ def test_cpp_host_reference_gpu_tests():
 def test_cpp_model_forward():
     out = _run("test_model", "gpu")
     assert "FAILED" not in out
-    for name in ("model_rejects_invalid_batches_like_the_reference", "decode_graphs_replay_the_eager_forward",
-                 "decode_step_matches_prefill_of_the_longer_prompt",
+    for name in ("plan_rejects_invalid_batches", "plan_fuses_attention_only_for_independent_rows",
+                 "forward_matches_the_oracle_stage_by_stage", "decode_graphs_replay_the_eager_forward",
+                 "fused_and_split_attention_give_identical_steps", "decode_step_matches_prefill_of_the_longer_prompt",
                  "model_reports_memory_and_keeps_graphs_per_batch_size"):
         assert name + " ..." in out

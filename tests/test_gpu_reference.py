@@ -1,6 +1,6 @@
 """The reference's own GPU tests (src/gpu.rs:1148-1472), restated over this
-library through the same wrapper API (nvr.Gpu mirrors src/gpu.rs), plus graph
-capture/replay of the fused kernels.
+library through the Python host API (nvr.Gpu has the reference host's object
+and method names), plus graph capture/replay of the fused kernels.
 
 """
 import math
@@ -26,16 +26,16 @@ def test_gpu_views_keep_allocations_and_reject_overlap():
     packed.upload(np.array([1, 3, 0, 0, 5, 6, 7, 8], np.int32))
     tokens = packed.slice(0, 8)
     adjacent = packed.slice(8, 8)
-    gpu.distinct(tokens, [adjacent])
-    with pytest.raises(ValueError):
-        gpu.distinct(tokens, [packed.slice(4, 8)])
-    with pytest.raises(ValueError):
+    assert not tokens.overlaps(adjacent) and tokens.overlaps(packed.slice(4, 8))
+    with pytest.raises(nvr.ArgumentError):
         tokens.slice(4, 8)
-    with pytest.raises(ValueError):
-        gpu.tensor(packed.slice(1, 8), [1], 4)
     weights = gpu.alloc(8)
     weights.upload(bf16_of([1.0, 2.0, 3.0, 4.0]))
     out = gpu.alloc(4)
+    with pytest.raises(nvr.ArgumentError, match="alignment"):  # a misaligned i32 view
+        gpu.embedding(packed.slice(1, 8), weights, out, 2, 1, 4)
+    with pytest.raises(nvr.ArgumentError, match="overlap"):  # the output is part of an input
+        gpu.embedding(tokens, weights, weights.slice(0, 4), 2, 1, 4)
     graph = gpu.capture(lambda: gpu.embedding(tokens, weights, out, 2, 1, 4))
     del tokens, adjacent, packed
     graph.replay()
@@ -125,7 +125,7 @@ def test_gpu_gemm_rms_sampling_graph():
     del x, w
     graph.replay()
     gpu.sync()
-    with pytest.raises(ValueError):
+    with pytest.raises(nvr.BackendError, match="allocation"):
         gpu.capture(lambda: gpu.alloc(4))
     gpu.sync()
 
@@ -233,7 +233,7 @@ def test_gpu_alloc_is_zero_filled_and_errors_carry_messages():
     assert 0 < free <= total
     assert gpu.sm_count() > 0
     with pytest.raises(nvr.BackendError, match="status -2"):
-        nvr._check(gpu.lib.nv_silu(gpu.handle, None, None, 0, 8))
+        nvr.check_status(gpu.lib.nv_silu(gpu.handle, None, None, 0, 8))
 
 
 def test_gpu_forward_chain_graph_replays_match_eager():
