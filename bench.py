@@ -244,7 +244,7 @@ def time_graph(gpu, hip, graph, reps, warmup):
 
 
 # ------------------------------------------------------ per-kernel loops ---
-def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain, only=()):
+def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=()):
     """(name, workload, launch closures over rotating sets, bytes per launch, rows per launch) per case."""
     cases = []
 
@@ -255,6 +255,16 @@ def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain, only=()):
         return max(3, -(-MALL_DEFEAT_BYTES // per_set_bytes))
 
     w = fill.normal(H * 2, 1.0, 0.02)
+    # A plain device-to-device copy of 256 MiB by the HIP runtime's own copy
+    # kernel: the counters' calibration and the copy rate of this GPU.
+    if want(COPY_CASE):
+        n = COPY_BYTES
+        srcs = [gpu.alloc(n) for _ in range(3)]
+        dsts = [gpu.alloc(n) for _ in range(3)]
+        stream = gpu.stream()
+        cases.append((COPY_CASE, "device-to-device copy of 256 MiB (HIP runtime copy kernel)",
+                      [lambda i=i: hip.copy_d2d(dsts[i].ptr, srcs[i].ptr, n, stream) for i in range(3)], 2 * n, 0))
+
     # RMSNorm 8 x 1024 (latency-bound decode shape).
     if want("rms_8x1024"):
         n = 64
@@ -426,36 +436,147 @@ def kernel_cases(gpu: nvr.Gpu, fill: Filler, chain: Chain, only=()):
     return cases
 
 
-def measured_traffic(case):
-    """HBM bytes per launch of `case` from the committed rocprofv3 counter
-    summary (FETCH_SIZE and WRITE_SIZE, scaled by a copy kernel of known
-    size), or None when the summary does not list it."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "pmc_traffic.txt")
+TRAFFIC_SUMMARY = os.path.join("profiles", "pmc_traffic.txt")
+VALU_SUMMARY = os.path.join("profiles", "sampling_valu.txt")
+SCLK_GHZ = 2.4  # MI355X peak engine clock
+
+COPY_CASE, COPY_BYTES = "copy_256mb", 256 << 20
+# The kernel each profiled case launches, as a substring of rocprofv3's Kernel_Name.
+CASE_KERNEL = {
+    COPY_CASE: "__amd_rocclr_copyBuffer",
+    "silu_8192x6144": "silu16",
+    "add_rms_8192x1024": "rms_rows_fast<4, true>",
+    "qkv_rope_8192": "qkv_rope_d128<true, 4>",
+    "embedding_16384": "gather_rows16",
+    "kv_write_16384": "kv_write16",
+    "attention_decode_64x4096": "attention_ordered<128, 2, 2, false, false>",
+    "sampling_256x151936": "sample_resident<",
+    "sampling_greedy": "sample_resident<",
+    "sampling_gumbel": "sample_resident<",
+}
+TRAFFIC_CASES = [COPY_CASE, "silu_8192x6144", "add_rms_8192x1024", "qkv_rope_8192", "embedding_16384",
+                 "kv_write_16384", "attention_decode_64x4096", "sampling_gumbel"]
+READ_COUNTERS = ["TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum"]
+WRITE_COUNTERS = ["TCC_EA0_WRREQ_sum", "TCC_EA0_WRREQ_64B_sum"]
+VALU_COUNTERS = ["SQ_INSTS_VALU", "SQ_WAVES", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_VMEM"]
+
+
+def summary_rows(path, width):
+    """{case: fields} from a committed summary table whose rows start with a case name."""
+    rows = {}
     try:
-        for line in open(path):
+        for line in open(os.path.join(ROOT, path)):
             tok = line.split()
-            if len(tok) >= 6 and tok[0] == case and tok[-3].isdigit():
-                return int(tok[-3])
+            if len(tok) == width and tok[0] in CASE_KERNEL and tok[-1].replace(".", "", 1).isdigit():
+                rows[tok[0]] = tok
     except OSError:
         pass
-    return None
+    return rows
 
 
-SCLK_GHZ = 2.4  # MI355X peak engine clock
+def measured_traffic(case):
+    """HBM bytes per launch of `case` in the committed traffic summary (TCC-to-memory
+    read and write requests by size, counted by rocprofv3), or None."""
+    row = summary_rows(TRAFFIC_SUMMARY, 7).get(case)
+    return int(row[4]) if row else None
 
 
 def measured_valu(case):
-    """VALU wave-instructions per launch of a sampling case from the committed
-    rocprofv3 SQ_INSTS_VALU summary, or None when the summary does not list it."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "sampling_valu.txt")
-    try:
-        for line in open(path):
-            tok = line.split()
-            if len(tok) >= 9 and tok[0] == case and tok[1].isdigit():
-                return int(tok[1])
-    except OSError:
-        pass
-    return None
+    """VALU wave-instructions per launch of a sampling case in the committed SQ
+    counter summary, or None."""
+    row = summary_rows(VALU_SUMMARY, 9).get(case)
+    return int(row[1]) if row else None
+
+
+def read_dispatches(directory):
+    """[(kernel name, grid size, {counter: value})] per dispatch in dispatch
+    order, from the rocprofv3 counter_collection.csv under `directory`."""
+    import csv
+    import glob
+
+    out = {}
+    for path in sorted(glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)):
+        with open(path, newline="") as f:
+            for rec in csv.DictReader(f):
+                key = (path, int(rec["Dispatch_Id"]))
+                name, grid = rec["Kernel_Name"], int(rec["Grid_Size"])
+                out.setdefault(key, (name, grid, {}))[2][rec["Counter_Name"]] = float(rec["Counter_Value"])
+    return [out[k] for k in sorted(out)]
+
+
+def case_dispatches(dispatches, case):
+    """The dispatches of `case`'s kernel. The runtime's copy kernel also fills
+    the buffers while the cases are set up, so the copy case runs last and its
+    dispatches are the copies after the last dispatch of any other kernel."""
+    if case != COPY_CASE:
+        return [d for d in dispatches if CASE_KERNEL[case] in d[0]]
+    tail = []
+    for d in reversed(dispatches):
+        if CASE_KERNEL[case] not in d[0]:
+            break
+        tail.append(d)
+    return tail[::-1]
+
+
+def pmc_summary(kind, dirs, cases_bytes):
+    """Prints the table of a counter pass (see --pmc-summary)."""
+    def mean(ds, f):
+        return sum(f(c) for _, _, c in ds) / len(ds)
+
+    if kind == "traffic":
+        rd, wr = read_dispatches(dirs[0]), read_dispatches(dirs[1])
+
+        def read_b(c):
+            return 32 * c["TCC_EA0_RDREQ_32B_sum"] + 64 * c["TCC_EA0_RDREQ_64B_sum"] + 128 * c["TCC_EA0_RDREQ_128B_sum"]
+
+        def write_b(c):
+            return 32 * (c["TCC_EA0_WRREQ_sum"] - c["TCC_EA0_WRREQ_64B_sum"]) + 64 * c["TCC_EA0_WRREQ_64B_sum"]
+
+        cr, cw = case_dispatches(rd, COPY_CASE), case_dispatches(wr, COPY_CASE)
+        rf, wf = COPY_BYTES / mean(cr, read_b), COPY_BYTES / mean(cw, write_b)
+        print(f"calibration: the {COPY_BYTES >> 20} MiB runtime copy ({len(cr)} + {len(cw)} dispatches) reads "
+              f"{mean(cr, read_b):.0f} B and writes {mean(cw, write_b):.0f} B by these counters: read factor "
+              f"{rf:.4f}, write factor {wf:.4f}")
+        print()
+        print(f"{'case':26s} {'kernel':38s} {'read B':>12s} {'write B':>12s} {'traffic B':>12s} "
+              f"{'algorithmic B':>13s} {'ratio':>6s}")
+        for case in TRAFFIC_CASES:
+            r, w = case_dispatches(rd, case), case_dispatches(wr, case)
+            if not r or not w:
+                continue
+            rb, wb = mean(r, read_b) * rf, mean(w, write_b) * wf
+            alg = cases_bytes[case]
+            print(f"{case:26s} {CASE_KERNEL[case].replace(' ', ''):38s} {rb:12.0f} {wb:12.0f} {rb + wb:12.0f} "
+                  f"{alg:13d} {(rb + wb) / alg:6.3f}")
+    else:
+        sq = read_dispatches(dirs[0])
+        print(f"{'case':26s} {'VALU':>9s} {'per wave':>9s} {'SALU':>9s} {'LDS':>9s} {'VMEM':>8s} {'waves':>7s} "
+              f"{'floor us':>9s} {'dispatches':>10s}")
+        # The three sampling cases share a kernel and run in this order, one
+        # after another, with the same number of dispatches each.
+        ds = case_dispatches(sq, "sampling_gumbel")
+        names = ["sampling_256x151936", "sampling_greedy", "sampling_gumbel"]
+        per = len(ds) // len(names)
+        for k, case in enumerate(names):
+            part = ds[k * per:(k + 1) * per]
+            if not part:
+                continue
+            valu, waves = mean(part, lambda c: c["SQ_INSTS_VALU"]), mean(part, lambda c: c["SQ_WAVES"])
+            floor = valu / (256 * SCLK_GHZ * 1e3)
+            print(f"{case:26s} {valu:9.0f} {valu / waves:9.0f} {mean(part, lambda c: c['SQ_INSTS_SALU']):9.0f} "
+                  f"{mean(part, lambda c: c['SQ_INSTS_LDS']):9.0f} {mean(part, lambda c: c['SQ_INSTS_VMEM']):8.0f} "
+                  f"{waves:7.0f} {floor:9.2f} {len(part):10d}")
+
+
+def traffic_case_bytes():
+    """Algorithmic bytes per launch of the traffic cases (the same figures the
+    kernel table uses; no device needed)."""
+    T = 8192
+    distinct = len(np.unique(np.random.default_rng(T).integers(0, MAX_POS, T)))
+    return {COPY_CASE: 2 * COPY_BYTES, "silu_8192x6144": bytes_silu(T, I), "add_rms_8192x1024": bytes_add_rms(T, H),
+            "qkv_rope_8192": bytes_qkv_rope(T, distinct), "embedding_16384": bytes_embedding(16384, H),
+            "kv_write_16384": bytes_kv_write(16384), "attention_decode_64x4096": bytes_attention(64, MAX_POS, MAX_POS // BS),
+            "sampling_gumbel": bytes_sampling(256, V)}
 
 
 def run_kernel_case(gpu, hip, launches, rounds):
@@ -565,7 +686,17 @@ def main() -> int:
     ap.add_argument("--no-decode", action="store_true", help="skip the forward runner's decode-step lines")
     ap.add_argument("--kernel-rounds", type=int, default=5)
     ap.add_argument("--only", default="", help="comma-separated kernel cases to run (implies --no-cpu, skips the step)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar=("KIND", "DIR"),
+                    help="print the table of rocprofv3 counter runs instead of measuring: 'traffic READ_DIR WRITE_DIR' "
+                         f"(passes of {' '.join(READ_COUNTERS)} and of {' '.join(WRITE_COUNTERS)}) or 'valu SQ_DIR' "
+                         f"(a pass of {' '.join(VALU_COUNTERS)})")
     args = ap.parse_args()
+    if args.pmc_summary:
+        kind, dirs = args.pmc_summary[0], args.pmc_summary[1:]
+        if (kind, len(dirs)) not in (("traffic", 2), ("valu", 1)):
+            ap.error("--pmc-summary takes 'traffic READ_DIR WRITE_DIR' or 'valu SQ_DIR'")
+        pmc_summary(kind, dirs, traffic_case_bytes())
+        return 0
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported "
               "(the kernels are per-token; a data-parallel split needs no collectives).", file=sys.stderr)
@@ -592,18 +723,26 @@ def main() -> int:
 
     kernels = {}
     if not args.no_kernels:
-        for name, workload, launches, nbytes, rows in kernel_cases(gpu, fill, chain, only):
+        cases = kernel_cases(gpu, hip, fill, chain, only)
+        # The calibration copy runs last (its dispatches are told from the
+        # set-up's copies by their place; see case_dispatches).
+        cases.sort(key=lambda c: c[0] == COPY_CASE)
+        for name, workload, launches, nbytes, rows in cases:
             t = run_kernel_case(gpu, hip, launches, args.kernel_rounds)
             gbs = nbytes / (t / 1e3) / 1e9
             kernels[name] = {"workload": workload, "us": round(t * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
                              "frac": round(gbs / HBM_PEAK_GBS, 4), "rows_per_s": round(rows / (t / 1e3), 1),
                              "launches": len(launches)}
+            traffic = measured_traffic(name)
+            if traffic is not None:
+                kernels[name]["traffic"] = {"bytes": traffic, "ratio": round(traffic / nbytes, 3),
+                                            "source": TRAFFIC_SUMMARY}
             valu = measured_valu(name)
             if valu is not None:
                 # VALU roofline: one wave64 VALU instruction per CU per cycle.
                 floor_us = valu / (gpu.sm_count() * SCLK_GHZ * 1e3)
                 kernels[name]["valu"] = {"insts": valu, "floor_us": round(floor_us, 2),
-                                         "frac": round(floor_us / (t * 1e3), 4)}
+                                         "frac": round(floor_us / (t * 1e3), 4), "source": VALU_SUMMARY}
 
     # Dominant kernel of the step: the largest share of the step's HBM bytes
     # (launches x algorithmic bytes at the step's shape). By time, SiLU and
@@ -616,7 +755,8 @@ def main() -> int:
         dom = max(share, key=share.get)
         kd = kernels[shape_of[dom]]
         roofline = {"kernel": shape_of[dom], "bound": "hbm", "achieved": kd["GB/s"], "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": kd["frac"], "traffic": measured_traffic(shape_of[dom])}
+                    "unit": "GB/s", "frac": kd["frac"], "traffic": measured_traffic(shape_of[dom]),
+                    "traffic_source": TRAFFIC_SUMMARY}
 
     cpu = None
     if not args.no_cpu and not only:

@@ -1,0 +1,98 @@
+"""The benchmark's counter summaries: traffic from TCC-to-memory request counts
+by size, calibrated by the runtime's 256 MiB copy, and the VALU table; and
+that the benchmark line reads those tables back (no GPU needed)."""
+import contextlib
+import csv
+import io
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+
+FIELDS = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id", "Grid_Size", "Kernel_Id",
+          "Kernel_Name", "Workgroup_Size", "LDS_Block_Size", "Scratch_Size", "VGPR_Count", "Accum_VGPR_Count",
+          "SGPR_Count", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+
+
+def write_pass(directory, dispatches):
+    """dispatches: [(kernel name, grid, {counter: value})] as rocprofv3 writes them."""
+    os.makedirs(directory, exist_ok=True)
+    with open(os.path.join(directory, "run_counter_collection.csv"), "w", newline="") as f:
+        w = csv.writer(f, quoting=csv.QUOTE_NONNUMERIC)
+        w.writerow(FIELDS)
+        for i, (name, grid, counters) in enumerate(dispatches, 1):
+            for counter, value in counters.items():
+                w.writerow([i, i, "Agent 1", 1, 1, 1, grid, i, name, 256, 0, 0, 32, 0, 32, counter, float(value), 0, 1])
+
+
+def run_summary(*args):
+    out = io.StringIO()
+    with contextlib.redirect_stdout(out):
+        bench.pmc_summary(*args)
+    return out.getvalue()
+
+
+def test_traffic_table_counts_request_sizes_and_applies_the_copy_calibration(tmp_path):
+    copy = bench.COPY_BYTES
+    silu = "void (anonymous namespace)::silu16(int)"
+    fill = ("__amd_rocclr_copyBuffer", 131072, {"TCC_EA0_RDREQ_32B_sum": 0, "TCC_EA0_RDREQ_64B_sum": 7,
+                                                 "TCC_EA0_RDREQ_128B_sum": 262144})  # set-up copies: ignored
+    rd = [fill, fill,
+          (silu, 999, {"TCC_EA0_RDREQ_32B_sum": 10, "TCC_EA0_RDREQ_64B_sum": 20, "TCC_EA0_RDREQ_128B_sum": 30}),
+          (silu, 999, {"TCC_EA0_RDREQ_32B_sum": 30, "TCC_EA0_RDREQ_64B_sum": 20, "TCC_EA0_RDREQ_128B_sum": 10}),
+          # the calibration copies run last and read 2% more than they should:
+          # every case is scaled by 1/1.02
+          ("__amd_rocclr_copyBuffer", 131072, {"TCC_EA0_RDREQ_32B_sum": 0, "TCC_EA0_RDREQ_64B_sum": 0,
+                                                "TCC_EA0_RDREQ_128B_sum": 1.02 * copy / 128})]
+    rd.append(rd[-1])
+    wr = [(silu, 999, {"TCC_EA0_WRREQ_sum": 100, "TCC_EA0_WRREQ_64B_sum": 40}),
+          ("__amd_rocclr_copyBuffer", 131072, {"TCC_EA0_WRREQ_sum": copy / 64, "TCC_EA0_WRREQ_64B_sum": copy / 64})]
+    write_pass(tmp_path / "rd", rd)
+    write_pass(tmp_path / "wr", wr)
+    alg = {case: 1000 for case in bench.TRAFFIC_CASES}
+    text = run_summary("traffic", [str(tmp_path / "rd"), str(tmp_path / "wr")], alg)
+    assert "read factor 0.9804" in text and "write factor 1.0000" in text
+    # silu: mean read = (32*20 + 64*20 + 128*20) = 4480 B, /1.02; write = 32*60 + 64*40 = 4480 B.
+    want_read, want_write = 4480 / 1.02, 4480
+    (tmp_path / "summary.txt").write_text(text)
+    rows = bench.summary_rows(str(tmp_path / "summary.txt"), 7)
+    assert set(rows) == {bench.COPY_CASE, "silu_8192x6144"}
+    silu = rows["silu_8192x6144"]
+    assert silu[1] == "silu16"
+    assert abs(float(silu[2]) - want_read) <= 0.5 and abs(float(silu[3]) - want_write) <= 0.5
+    assert int(silu[4]) == round(want_read + want_write)
+    assert abs(float(silu[6]) - (want_read + want_write) / 1000) < 1e-3
+    assert int(rows[bench.COPY_CASE][4]) == 2 * copy  # the copy reads itself back exactly
+
+
+def test_valu_table_splits_the_sampling_cases_in_launch_order(tmp_path):
+    name = "void (anonymous namespace)::sample_resident<20, 1024>(...)"
+    ds = []
+    for valu in (100, 200, 300):  # mixed, greedy, Gumbel: two dispatches each
+        for _ in range(2):
+            ds.append((name, 1 << 18, {"SQ_INSTS_VALU": valu * 1e6, "SQ_WAVES": 4096, "SQ_INSTS_SALU": 1,
+                                       "SQ_INSTS_LDS": 2, "SQ_INSTS_VMEM": 3}))
+    write_pass(tmp_path / "sq", ds)
+    text = run_summary("valu", [str(tmp_path / "sq")], {})
+    (tmp_path / "valu.txt").write_text(text)
+    rows = bench.summary_rows(str(tmp_path / "valu.txt"), 9)
+    assert {k: int(v[1]) for k, v in rows.items()} == {"sampling_256x151936": 100_000_000,
+                                                       "sampling_greedy": 200_000_000,
+                                                       "sampling_gumbel": 300_000_000}
+    assert rows["sampling_gumbel"][-1] == "2"
+
+
+def test_committed_summaries_feed_the_benchmark_line():
+    traffic = {case: bench.measured_traffic(case) for case in bench.TRAFFIC_CASES}
+    alg = bench.traffic_case_bytes()
+    for case, b in traffic.items():
+        if b is None:
+            pytest.fail(f"{bench.TRAFFIC_SUMMARY} has no row for {case}")
+        assert 0.9 < b / alg[case] < 1.2, (case, b, alg[case])
+    for case in ("sampling_256x151936", "sampling_greedy", "sampling_gumbel"):
+        assert bench.measured_valu(case) is not None, case
