@@ -445,10 +445,33 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
             acc = __builtin_fmaf(p1.w, v[7], acc);
         };
         if (n == kVTile) {
-            // A whole tile, unrolled, so the LDS reads of later tokens are
-            // issued ahead of the chain instead of one round trip per 8 tokens.
+            // A whole tile, software-pipelined: the LDS reads of the next 8
+            // tokens are issued before the current 8 are chained, so each
+            // group's LDS round trip hides behind the previous group's FMAs.
+            float pa[8], pb[8];
+            uint32_t va[8], vb[8];
+            auto fetch = [&](int j, float (&p)[8], uint32_t (&v)[8]) {
+                const float4 p0 = *reinterpret_cast<const float4*>(pg + t0 + j);
+                const float4 p1 = *reinterpret_cast<const float4*>(pg + t0 + j + 4);
+                p[0] = p0.x; p[1] = p0.y; p[2] = p0.z; p[3] = p0.w;
+                p[4] = p1.x; p[5] = p1.y; p[6] = p1.z; p[7] = p1.w;
 #pragma unroll
-            for (int j = 0; j < kVTile; j += 8) eight(j);
+                for (int k = 0; k < 8; ++k) v[k] = vt[(j + k) * DIM];
+            };
+            auto chain8 = [&](const float (&p)[8], const uint32_t (&v)[8]) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc = __builtin_fmaf(p[k], __uint_as_float(v[k] << 16), acc);
+            };
+            fetch(0, pa, va);
+#pragma unroll
+            for (int j = 0; j < kVTile; j += 16) {
+                fetch(j + 8, pb, vb);
+                __builtin_amdgcn_sched_barrier(0);
+                chain8(pa, va);
+                if (j + 16 < kVTile) fetch(j + 16, pa, va);
+                __builtin_amdgcn_sched_barrier(0);
+                chain8(pb, vb);
+            }
             return;
         }
         int j = 0;
