@@ -92,6 +92,17 @@ int nv_rms(nv_context* c, const void* x, const void* weight, void* out,
 int nv_add_rms(nv_context* c, const void* x, void* residual, const void* weight, void* out,
                int rows, int hidden, float eps);
 
+/* The final add-RMSNorm and the last-token gather of src/model.rs:781-797 in
+ * one launch (no single reference entry point: nv_add_rms, kernels/kernels.cu:471,
+ * followed by nv_gather, :487). For output row r with i = indices[r] in
+ * [0, input_rows): out[r] = nv_add_rms's output row i; other indices give a
+ * +0 row. Only gathered rows are computed, and the residual is read, not
+ * updated (nothing reads it after the final norm), so rows may repeat.
+ * x and residual are [input_rows, hidden], out is [rows, hidden]. */
+int nv_add_rms_gather(nv_context* c, const void* x, const void* residual, const void* weight,
+                      const void* indices, void* out, int rows, int hidden, int input_rows,
+                      float eps);
+
 /* kernels/kernels.cu:166-211,472 — per-head q/k RMSNorm, NeoX RoPE with the
  * angle computed inline, q -> qout, k/v -> paged caches at slots[r]
  * (src/gpu.rs:661-706). qkv is [rows, qh + 2*kvh, dim]; caches are

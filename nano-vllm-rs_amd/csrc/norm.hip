@@ -24,6 +24,13 @@
 // two-source bf16 pack measured slower for this kernel on MI355X.)
 // Generic path (any hidden, any alignment): one row per wave, lane l owns
 // reference threads 4l..4l+3 with 2-byte accesses.
+//
+// GATHER (nv_add_rms_gather): output row r is input row index[r] — the final
+// add-RMSNorm and the last-token gather of src/model.rs:781-797 in one
+// launch, computed for the gathered rows only. The residual is only read
+// (after the final norm nothing reads it), so a row may be gathered any
+// number of times. An index outside [0, input_rows) gives a +0 row (the
+// gather's rule, kernels/kernels.cu:366-371).
 #include "../../include/nano_hip.h"
 #include "nvr_device.h"
 #include "nvr_internal.h"
@@ -32,15 +39,26 @@ namespace {
 
 using nvr::kWave;
 
-template <int K, bool ADD>
+template <int K, bool ADD, bool GATHER = false>
 __global__ __launch_bounds__(256) void rms_rows_fast(const uint16_t* __restrict__ x, uint16_t* __restrict__ residual,
                                                      const uint16_t* __restrict__ weight, uint16_t* __restrict__ out,
-                                                     int rows, int hidden, float eps) {
+                                                     int rows, int hidden, float eps,
+                                                     const int* __restrict__ index = nullptr, int input_rows = 0) {
     const int lane = threadIdx.x & (kWave - 1);
     const int m = lane & 31;
     const int64_t row = (int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave) * 2 + (lane >> 5);
-    const bool active = row < rows;
-    const int64_t base = row * hidden + 8 * m;
+    int64_t src = row;
+    bool active = row < rows;
+    if constexpr (GATHER) {
+        src = active ? index[row] : -1;
+        if (active && (src < 0 || src >= input_rows)) {  // the gather's +0 row
+#pragma unroll
+            for (int k = 0; k < K; ++k) nvr::store_stream(out + row * hidden + 8 * m + 256 * k, make_uint4(0, 0, 0, 0));
+            active = false;
+        }
+    }
+    const int64_t base = src * hidden + 8 * m;     // input and residual row
+    const int64_t obase = row * hidden + 8 * m;    // output row
 
     float v[K][8];
     if (active) {
@@ -98,22 +116,31 @@ __global__ __launch_bounds__(256) void rms_rows_fast(const uint16_t* __restrict_
         nvr::unpack8(*reinterpret_cast<const uint4*>(weight + 256 * k + 8 * m), wf);
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = (v[k][i] * inv) * wf[i];
-        if constexpr (ADD) nvr::store_stream(residual + base + 256 * k, nvr::pack8_split(v[k]));
-        nvr::store_stream(out + base + 256 * k, nvr::pack8_split(o));
+        if constexpr (ADD && !GATHER) nvr::store_stream(residual + base + 256 * k, nvr::pack8_split(v[k]));
+        nvr::store_stream(out + obase + 256 * k, nvr::pack8_split(o));
     }
 }
 
 // Any hidden size, 2-byte alignment. One row per wave; lane l plays reference
 // threads 4l..4l+3: warp w = lanes 8w..8w+7, so warp level 16 -> lane ^4,
 // 8 -> ^2, 4 -> ^1, 2/1 in-lane; block level 4 -> ^32, 2 -> ^16, 1 -> ^8.
-template <bool ADD>
+template <bool ADD, bool GATHER = false>
 __global__ __launch_bounds__(256) void rms_rows_generic(const uint16_t* __restrict__ x, uint16_t* __restrict__ residual,
                                                         const uint16_t* __restrict__ weight,
-                                                        uint16_t* __restrict__ out, int rows, int hidden, float eps) {
+                                                        uint16_t* __restrict__ out, int rows, int hidden, float eps,
+                                                        const int* __restrict__ index = nullptr, int input_rows = 0) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
     if (row >= rows) return;  // whole wave exits together
-    const int64_t base = row * hidden;
+    int64_t src = row;
+    if constexpr (GATHER) {
+        src = index[row];
+        if (src < 0 || src >= input_rows) {  // the gather's +0 row
+            for (int j = lane; j < hidden; j += kWave) out[row * hidden + j] = 0;
+            return;
+        }
+    }
+    const int64_t base = src * hidden, obase = row * hidden;
     float s[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -140,25 +167,27 @@ __global__ __launch_bounds__(256) void rms_rows_generic(const uint16_t* __restri
         float v = nvr::bf16_to_f32(x[base + j]);
         if constexpr (ADD) {
             v += nvr::bf16_to_f32(residual[base + j]);
-            residual[base + j] = nvr::f32_to_bf16(v);
+            if constexpr (!GATHER) residual[base + j] = nvr::f32_to_bf16(v);
         }
-        out[base + j] = nvr::f32_to_bf16((v * inv) * nvr::bf16_to_f32(weight[j]));
+        out[obase + j] = nvr::f32_to_bf16((v * inv) * nvr::bf16_to_f32(weight[j]));
     }
 }
 
-template <int K, bool ADD>
+template <int K, bool ADD, bool GATHER>
 void launch_fast(hipStream_t stream, const uint16_t* x, uint16_t* res, const uint16_t* w, uint16_t* out, int rows,
-                 int hidden, float eps) {
+                 int hidden, float eps, const int* index, int input_rows) {
     const int rows_per_block = 8;  // 4 waves x 2 rows
     const unsigned blocks = unsigned((int64_t(rows) + rows_per_block - 1) / rows_per_block);
-    hipLaunchKernelGGL((rms_rows_fast<K, ADD>), dim3(blocks), dim3(256), 0, stream, x, res, w, out, rows, hidden, eps);
+    hipLaunchKernelGGL((rms_rows_fast<K, ADD, GATHER>), dim3(blocks), dim3(256), 0, stream, x, res, w, out, rows,
+                       hidden, eps, index, input_rows);
 }
 
-template <bool ADD>
+template <bool ADD, bool GATHER = false>
 int launch_rms(nv_context* c, const void* xv, void* resv, const void* wv, void* outv, int rows, int hidden,
-               float eps) {
+               float eps, const int* index = nullptr, int input_rows = 0) {
     NVR_ACTIVATE(c);
     if (rows <= 0 || hidden <= 0) return nvr::fail(-2, "rms: rows and hidden must be positive");
+    if (GATHER && input_rows <= 0) return nvr::fail(-2, "add_rms_gather: input rows must be positive");
     auto x = static_cast<const uint16_t*>(xv);
     auto res = static_cast<uint16_t*>(resv);
     auto w = static_cast<const uint16_t*>(wv);
@@ -170,23 +199,23 @@ int launch_rms(nv_context* c, const void* xv, void* resv, const void* wv, void* 
                 K == 14 || K == 16 || K == 20)) {
         hipStream_t s = c->stream;
         switch (K) {
-            case 1: launch_fast<1, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            case 2: launch_fast<2, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            case 3: launch_fast<3, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            case 4: launch_fast<4, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            case 5: launch_fast<5, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            case 6: launch_fast<6, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            case 8: launch_fast<8, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            case 10: launch_fast<10, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            case 12: launch_fast<12, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            case 14: launch_fast<14, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            case 16: launch_fast<16, ADD>(s, x, res, w, out, rows, hidden, eps); break;
-            default: launch_fast<20, ADD>(s, x, res, w, out, rows, hidden, eps); break;
+            case 1: launch_fast<1, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            case 2: launch_fast<2, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            case 3: launch_fast<3, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            case 4: launch_fast<4, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            case 5: launch_fast<5, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            case 6: launch_fast<6, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            case 8: launch_fast<8, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            case 10: launch_fast<10, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            case 12: launch_fast<12, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            case 14: launch_fast<14, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            case 16: launch_fast<16, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
+            default: launch_fast<20, ADD, GATHER>(s, x, res, w, out, rows, hidden, eps, index, input_rows); break;
         }
     } else {
         const unsigned blocks = unsigned((int64_t(rows) + 3) / 4);
-        hipLaunchKernelGGL((rms_rows_generic<ADD>), dim3(blocks), dim3(256), 0, c->stream, x, res, w, out, rows,
-                           hidden, eps);
+        hipLaunchKernelGGL((rms_rows_generic<ADD, GATHER>), dim3(blocks), dim3(256), 0, c->stream, x, res, w, out,
+                           rows, hidden, eps, index, input_rows);
     }
     return nvr::launch_status();
 }
@@ -202,6 +231,14 @@ int nv_rms(nv_context* c, const void* x, const void* weight, void* out, int rows
 int nv_add_rms(nv_context* c, const void* x, void* residual, const void* weight, void* out, int rows, int hidden,
                float eps) {
     return launch_rms<true>(c, x, residual, weight, out, rows, hidden, eps);
+}
+
+int nv_add_rms_gather(nv_context* c, const void* x, const void* residual, const void* weight, const void* indices,
+                      void* out, int rows, int hidden, int input_rows, float eps) {
+    // The gather form never writes the residual (the kernel's pointer is
+    // non-const only for the shared template).
+    return launch_rms<true, true>(c, x, const_cast<void*>(residual), weight, out, rows, hidden, eps,
+                                  static_cast<const int*>(indices), input_rows);
 }
 
 }  // extern "C"

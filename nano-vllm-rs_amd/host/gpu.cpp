@@ -303,6 +303,19 @@ void Gpu::add_rms_norm(const Buffer& x, const Buffer& residual, const Buffer& we
                               as_dim(rows), as_dim(hidden), eps));
 }
 
+void Gpu::add_rms_norm_gather(const Buffer& x, const Buffer& residual, const Buffer& weight, const Buffer& indices,
+                              const Buffer& out, std::size_t rows, std::size_t hidden, std::size_t input_rows,
+                              float eps) const {
+    require_positive(eps, "add_rms_norm_gather eps");
+    admit("add_rms_norm_gather",
+          {read_arg("x", x, 2, {input_rows, hidden}), read_arg("residual", residual, 2, {input_rows, hidden}),
+           read_arg("weight", weight, 2, {hidden}), read_arg("indices", indices, 4, {rows}),
+           write_arg("out", out, 2, {rows, hidden})});
+    require_status(nv_add_rms_gather(context(), x.address(), residual.address(), weight.address(),
+                                     indices.address(), out.address(), as_dim(rows), as_dim(hidden),
+                                     as_dim(input_rows), eps));
+}
+
 namespace {
 // The arguments shared by the q/k norm + RoPE + KV write kernels.
 struct RopeShape {

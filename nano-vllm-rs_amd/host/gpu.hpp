@@ -175,6 +175,11 @@ public:
     // residual <- bf16(x + residual); out <- RMSNorm(f32(x) + f32(residual)).
     void add_rms_norm(const Buffer& x, const Buffer& residual, const Buffer& weight, const Buffer& out,
                       std::size_t rows, std::size_t hidden, float eps) const;
+    // add_rms_norm's output for input rows indices[r] in output row r (+0
+    // rows for indices outside [0, input_rows)); residual is only read.
+    void add_rms_norm_gather(const Buffer& x, const Buffer& residual, const Buffer& weight, const Buffer& indices,
+                             const Buffer& out, std::size_t rows, std::size_t hidden, std::size_t input_rows,
+                             float eps) const;
     void qkv_rope(const Buffer& qkv, const Buffer& qweight, const Buffer& kweight, const Buffer& positions,
                   const Buffer& slots, const Buffer& qout, const Buffer& kcache, const Buffer& vcache,
                   std::size_t rows, std::size_t qheads, std::size_t kvheads, std::size_t head_dim,

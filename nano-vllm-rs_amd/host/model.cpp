@@ -350,10 +350,12 @@ void QwenModel::decoder_layer(const StepPlan& p, std::size_t i) const {
 void QwenModel::head(const StepPlan& p) const {
     const ModelConfig& c = config_;
     const Workspace& w = work_;
-    gpu_.add_rms_norm(w.hidden, w.residual, final_norm_, w.normed, p.rows, c.hidden_size, c.rms_norm_eps);
+    // The final add-RMSNorm computed for the sampled rows only, straight
+    // into the gathered buffer (one launch instead of a norm over every row
+    // and a gather).
+    gpu_.add_rms_norm_gather(w.hidden, w.residual, final_norm_, w.last_rows, w.gathered, p.samples, c.hidden_size,
+                             p.rows, c.rms_norm_eps);
     observe(Stage::FinalNorm);
-    gpu_.gather(w.normed, w.last_rows, w.gathered, p.samples, c.hidden_size, p.rows);
-    observe(Stage::Gathered);
     gpu_.gemm(w.gathered, lm_head_, w.logits, p.samples, c.vocab_size, c.hidden_size);
     observe(Stage::Logits);
     gpu_.sample_parallel(w.logits, w.temperatures, w.seeds, w.samples, w.partial_scores, w.partial_ids, p.samples,

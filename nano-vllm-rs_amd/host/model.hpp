@@ -150,8 +150,7 @@ enum class Stage {
     GateUp,      // gate_up GEMM output
     Activated,   // SiLU(gate) * up
     Down,        // hidden = down GEMM output
-    FinalNorm,   // residual and normed after the final add-RMSNorm
-    Gathered,    // the sampled rows of normed
+    FinalNorm,   // gathered = the final add-RMSNorm of the sampled rows (residual not updated)
     Logits,      // lm_head GEMM output
     Sampled,     // sampled token ids
 };

@@ -66,6 +66,7 @@ SIGNATURES = {
     "nv_embedding": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "nv_rms": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
     "nv_add_rms": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _f]),
+    "nv_add_rms_gather": (_i, [_vp] * 6 + [_i, _i, _i, _f]),
     "nv_qkv_rope": (_i, [_vp] * 9 + [_i] * 6 + [_f, _f]),
     "nv_rope_cache": (_i, [_vp, _vp, _i, _i, _f]),
     "nv_qkv_rope_cached": (_i, [_vp] * 9 + [_i] * 6 + [_f, _vp, _i]),
@@ -395,6 +396,17 @@ class Gpu:
         self._admit("add_rms_norm", [_r("x", x, 2, rows, hidden), _w("residual", residual, 2, rows, hidden),
                                      _r("weight", weight, 2, hidden), _w("out", out, 2, rows, hidden)])
         self._call(self.lib.nv_add_rms(self.handle, x.ptr, residual.ptr, weight.ptr, out.ptr, rows, hidden, eps))
+
+    def add_rms_norm_gather(self, x: Buffer, residual: Buffer, weight: Buffer, indices: Buffer, out: Buffer,
+                            rows: int, hidden: int, input_rows: int, eps: float) -> None:
+        """The output of add_rms_norm for input rows indices[r] in output row r (a +0 row for an index
+        outside [0, input_rows)); residual is read, not updated."""
+        require_positive(eps, "add_rms_norm_gather eps")
+        self._admit("add_rms_norm_gather", [
+            _r("x", x, 2, input_rows, hidden), _r("residual", residual, 2, input_rows, hidden),
+            _r("weight", weight, 2, hidden), _r("indices", indices, 4, rows), _w("out", out, 2, rows, hidden)])
+        self._call(self.lib.nv_add_rms_gather(self.handle, x.ptr, residual.ptr, weight.ptr, indices.ptr, out.ptr,
+                                              rows, hidden, input_rows, eps))
 
     @staticmethod
     def _rope_args(qkv, qweight, kweight, positions, slots, qout, kcache, vcache, rows, qheads, kvheads, head_dim,

@@ -410,12 +410,24 @@ struct OracleShadow {
             hidden = down16(w.hidden, rows * c.hidden_size);
             break;
         case Stage::PostNorm:
-        case Stage::FinalNorm: {
-            const std::vector<uint16_t>& weight = stage == Stage::PostNorm ? post_norm[l] : final_norm;
-            ora_add_rms(hidden.data(), residual.data(), weight.data(), normed.data(), R, H, c.rms_norm_eps,
+            ora_add_rms(hidden.data(), residual.data(), post_norm[l].data(), normed.data(), R, H, c.rms_norm_eps,
                         int(threads));
             CHECK_SAME(down16(w.residual, residual.size()), residual, 0, at + "add-norm residual");
             CHECK_SAME(down16(w.normed, normed.size()), normed, 0, at + "add-norm");
+            break;
+        case Stage::FinalNorm: {
+            // The runner computes the final add-RMSNorm for the sampled rows
+            // only, straight into the gathered rows: those must equal the
+            // oracle's norm over every row followed by the gather, and the
+            // residual is left as it was.
+            const std::vector<uint16_t> before = residual;
+            ora_add_rms(hidden.data(), residual.data(), final_norm.data(), normed.data(), R, H, c.rms_norm_eps,
+                        int(threads));
+            const std::size_t n = b.last_token_indices.size();
+            gathered.resize(n * c.hidden_size);
+            ora_gather(normed.data(), b.last_token_indices.data(), gathered.data(), int(n), H, R, int(threads));
+            CHECK_SAME(down16(w.gathered, gathered.size()), gathered, 0, "final norm of the sampled rows");
+            CHECK_SAME(down16(w.residual, before.size()), before, 0, "final norm residual");
             break;
         }
         case Stage::GateUp: {
@@ -427,13 +439,6 @@ struct OracleShadow {
         case Stage::Activated:
             CHECK_SAME(down16(w.activated, act.size()), act, 1, at + "SiLU");
             break;
-        case Stage::Gathered: {
-            const std::size_t n = b.last_token_indices.size();
-            gathered.resize(n * c.hidden_size);
-            ora_gather(normed.data(), b.last_token_indices.data(), gathered.data(), int(n), H, R, int(threads));
-            CHECK_SAME(down16(w.gathered, gathered.size()), gathered, 0, "last-row gather");
-            break;
-        }
         case Stage::Logits: {
             const std::size_t n = b.last_token_indices.size(), V = c.vocab_size, K = c.hidden_size;
             logits = down16(w.logits, n * V);
@@ -513,7 +518,7 @@ TEST(forward_matches_the_oracle_stage_by_stage, "gpu") {
     shadow.rows = prefill.token_ids.size();
     const std::vector<uint32_t> first = model.run(prefill);
     std::printf("[prefill: %zu stages] ", shadow.stages);
-    CHECK(shadow.stages == 1 + 3 * 9 + 4);  // split attention (a QkvRope stage) in the prefill
+    CHECK(shadow.stages == 1 + 3 * 9 + 3);  // split attention (a QkvRope stage) in the prefill
     std::vector<std::vector<int32_t>> next(S);
     std::vector<int32_t> at(S, int32_t(P));
     for (std::size_t s = 0; s < S; ++s) {
@@ -527,7 +532,7 @@ TEST(forward_matches_the_oracle_stage_by_stage, "gpu") {
     shadow.stages = 0;
     model.run(decode);
     std::printf("[decode: %zu stages] ", shadow.stages);
-    CHECK(shadow.stages == 1 + 3 * 8 + 4);  // fused attention: no QkvRope stage
+    CHECK(shadow.stages == 1 + 3 * 8 + 3);  // fused attention: no QkvRope stage
 }
 
 // ------------------------------------------------------ runner behaviour ---

@@ -92,6 +92,36 @@ def test_rms_generic_path_misaligned(gpu, hidden):
     assert_bits_equal(down(out, np.uint16, (rows, hidden)), want_out)
 
 
+@pytest.mark.parametrize("input_rows,hidden,align,picks", [
+    (1024, 1024, True, "last"),     # a prefill's last tokens of 8 sequences of 128
+    (8, 1024, True, "all"),         # a decode step: every row sampled
+    (40, 2048, True, "ragged"),     # duplicates and indices outside the input
+    (9, 1000, False, "ragged"),     # the generic path
+])
+def test_add_rms_gather_equals_add_rms_then_gather(gpu, input_rows, hidden, align, picks):
+    """nv_add_rms_gather against the oracle's add-RMSNorm over every row followed by
+    the gather; the residual is read, not written."""
+    rng = np.random.default_rng(input_rows + hidden)
+    if picks == "last":
+        idx = np.arange(127, input_rows, 128, dtype=np.int32)
+    elif picks == "all":
+        idx = np.arange(input_rows, dtype=np.int32)
+    else:
+        idx = rng.integers(-2, input_rows + 2, 13).astype(np.int32)
+        idx[[0, 5]] = idx[3]  # one row gathered three times
+    rows = len(idx)
+    x = ora.normal_bf16((input_rows, hidden), 11 + hidden)
+    res = ora.normal_bf16((input_rows, hidden), 12 + hidden)
+    w = ora.normal_bf16(hidden, 13, 1.0, 0.02)
+    put = up if align else misaligned
+    rb = put(gpu, res)
+    out = put(gpu, np.full((rows, hidden), 0x7FC1, np.uint16))
+    gpu.add_rms_norm_gather(put(gpu, x), rb, put(gpu, w), up(gpu, idx), out, rows, hidden, input_rows, EPS)
+    _, full_out = ora.add_rms(x, res, w, input_rows, hidden, EPS, threads=8)
+    assert_bits_equal(down(out, np.uint16, (rows, hidden)), ora.gather(full_out, idx, rows, hidden, input_rows))
+    assert_bits_equal(down(rb, np.uint16, (input_rows, hidden)), res.reshape(input_rows, hidden))
+
+
 # ------------------------------------------------------------------- RoPE ----
 def test_rope_table_bit_exact(gpu):
     table = gpu.alloc(4096 * 128 * 4)
