@@ -103,6 +103,21 @@ int nv_add_rms_gather(nv_context* c, const void* x, const void* residual, const 
                       const void* indices, void* out, int rows, int hidden, int input_rows,
                       float eps);
 
+/* No single counterpart in the reference: nv_rms / nv_add_rms
+ * (kernels/kernels.cu:145-164,470-471) followed by nv_gemm (:98-106) on the
+ * normalised rows, in one launch for decode-sized batches
+ * (src/model.rs:659-678 and :753-770). With residual == NULL, X = RMSNorm(x);
+ * otherwise v = x + residual, residual_out <- bf16(v) (a different buffer from
+ * residual; may be NULL) and X = RMSNorm(v), both exactly as nv_add_rms.
+ * Then y[m, n] = bf16(X W^T) with fp32 accumulation in a fixed order (not
+ * hipBLAS's: equal to nv_gemm to fp32 rounding). normed (may be NULL) receives
+ * X. Limits (else -2): 1 <= m <= 32, n a multiple of 16, k in {512, 1024, 2048},
+ * 16-byte aligned tensors. x, residual, residual_out, normed: [m, k];
+ * w: [n, k]; y: [m, n]. */
+int nv_rms_gemm(nv_context* c, const void* x, const void* residual, void* residual_out,
+                const void* norm_weight, const void* w, void* y, void* normed, int m, int n, int k,
+                float eps);
+
 /* kernels/kernels.cu:166-211,472 — per-head q/k RMSNorm, NeoX RoPE with the
  * angle computed inline, q -> qout, k/v -> paged caches at slots[r]
  * (src/gpu.rs:661-706). qkv is [rows, qh + 2*kvh, dim]; caches are

@@ -1,0 +1,249 @@
+// RMSNorm (or residual-add + RMSNorm) fused into the GEMM that consumes it,
+// for decode-sized batches (nv_rms_gemm).
+//
+// Semantics: the norm of kernels/kernels.cu:145-164 (nv_rms / nv_add_rms,
+// bit for bit: the same arithmetic and summation order as norm.hip) followed
+// by the GEMM of :98-106, Y[m, n] = bf16(sum_k X[m, k] W[n, k]) with fp32
+// accumulation, where X is the norm's bf16 output. This is the pair
+// src/model.rs:659-678 (input norm, qkv projection) and :753-770
+// (post-attention norm, gate_up projection) in one launch.
+//
+// Why: at 8-32 decode rows a norm is one memory round trip plus a launch
+// (~3.5 us) and the GEMM that follows streams its weights in a few us; fusing
+// them removes a launch and overlaps the norm with the weight stream.
+//
+// Layout (256 threads, column tile of 16 outputs per block, n / 16 blocks):
+//  1. Each half-wave issues the loads of its first input row (x, residual),
+//     then every wave its share of the tile's weights: wave w owns the k range
+//     [w k/4, (w+1) k/4) and lane l loads, for each 32-wide k step, the 16
+//     bytes W[n0 + l % 16][k0 + 8 (l / 16) ..] — the B operand layout of
+//     v_mfma_f32_16x16x32_bf16 (B[k][j] with k = 8 (l / 16) + e, j = l % 16).
+//     Loads retire in issue order, so the norm waits only for its rows.
+//  2. While the weights stream in, the block normalises the m input rows (one
+//     row per half-wave per pass of 8 rows, the layout and reduction tree of
+//     norm.hip's rms_rows_fast) into an LDS tile X[16 or 32][k] (rows >= m
+//     zero). Block 0 also writes residual_out (bf16(x + residual)) and, when
+//     asked, the normalised rows.
+//  3. Each wave runs its k steps on MFMA: A = X[l % 16 (+16)][k0 + 8 (l / 16) ..]
+//     from LDS, one accumulator tile per 16 rows.
+//  4. The four waves' partial tiles are summed through LDS in wave order and
+//     rounded once to bf16.
+// The GEMM's summation order (MFMA's, then the four k quarters in order) is
+// fixed, so every launch gives the same bits; it is not hipBLAS's order, so
+// the result matches nv_gemm's to fp32 rounding (checked against the float64
+// product's bound), while the norm outputs match the oracle bit for bit.
+// The residual is read from one buffer and written to another: a block that
+// updated it in place would race with blocks still reading it.
+#include "../../include/nano_hip.h"
+#include "nvr_device.h"
+#include "nvr_internal.h"
+
+namespace {
+
+using nvr::kWave;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256, kWaves = kThreads / kWave;
+constexpr int kTileN = 16;      // output columns per block (MFMA N)
+constexpr int kMaxRows = 32;    // two MFMA row tiles
+constexpr int kRowPad = 8;      // bf16 elements of padding per LDS row (spreads the A reads over the banks)
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// KC = k / 256 (16-byte chunks per lane of a half-wave row); MT = row tiles.
+template <int KC, int MT, bool ADD>
+__global__ __launch_bounds__(kThreads) void rms_gemm(const uint16_t* __restrict__ x,
+                                                     const uint16_t* __restrict__ residual,
+                                                     uint16_t* __restrict__ residual_out,
+                                                     const uint16_t* __restrict__ norm_weight,
+                                                     const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
+                                                     uint16_t* __restrict__ normed, int m, int n, float eps) {
+    constexpr int K = 256 * KC, KW = K / kWaves, STEPS = KW / 32, LDX = K + kRowPad;
+    extern __shared__ __align__(16) unsigned char smem[];
+    uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                          // [MT * 16][LDX]
+    float* red = reinterpret_cast<float*>(smem + sizeof(uint16_t) * MT * 16 * LDX);  // [kWaves][MT][256]
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int n0 = blockIdx.x * kTileN;
+
+    // 1. The first pass's input rows, then the tile's weights: all in flight
+    // before anything waits, and the norm (which waits only for the rows,
+    // issued first) overlaps the weight stream.
+    const int half = lane >> 5, hm = lane & 31;
+    const bool writer = blockIdx.x == 0;
+    const int passes = (m + 7) / 8;  // uniform; rows of a pass: pass * 8 + (wave * 2 + half)
+    auto row_of = [&](int pass) { return pass * 8 + wave * 2 + half; };
+    auto base_of = [&](int pass) { return int64_t(row_of(pass) < m ? row_of(pass) : 0) * K + 8 * hm; };
+    uint4 xw[KC], rw[KC];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) xw[c] = nvr::load_stream(x + base_of(0) + 256 * c);
+    if constexpr (ADD) {
+#pragma unroll
+        for (int c = 0; c < KC; ++c) rw[c] = *reinterpret_cast<const uint4*>(residual + base_of(0) + 256 * c);
+    }
+    const int kb = wave * KW;
+    uint4 wv[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s)
+        wv[s] = nvr::load_stream(w + int64_t(n0 + lane % 16) * K + kb + 32 * s + 8 * (lane / 16));
+
+    // 2. The norm of every input row into LDS (rms_rows_fast's arithmetic);
+    // row tiles past the last pass are zero.
+    if (passes < MT * 2) {
+        for (int i = threadIdx.x; i < (MT * 2 - passes) * 8 * (K / 8); i += kThreads) {
+            const int row = passes * 8 + i / (K / 8), col = 8 * (i % (K / 8));
+            *reinterpret_cast<uint4*>(xs + row * LDX + col) = make_uint4(0, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int pass = 0; pass < MT * 2; ++pass) {
+        if (pass >= passes) break;  // uniform
+        const int row = row_of(pass);
+        const bool active = row < m;
+        const int64_t base = base_of(pass);
+        if (pass > 0) {
+#pragma unroll
+            for (int c = 0; c < KC; ++c) xw[c] = nvr::load_stream(x + base + 256 * c);
+            if constexpr (ADD) {
+#pragma unroll
+                for (int c = 0; c < KC; ++c) rw[c] = *reinterpret_cast<const uint4*>(residual + base + 256 * c);
+            }
+        }
+        float v[KC][8];
+        if constexpr (ADD) {
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                float a[8], b[8];
+                nvr::unpack8(xw[c], a);
+                nvr::unpack8(rw[c], b);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[c][i] = active ? a[i] + b[i] : 0.0f;
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < KC; ++c) {
+                nvr::unpack8(xw[c], v[c]);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[c][i] = active ? v[c][i] : 0.0f;
+            }
+        }
+        float s[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < KC; ++c) acc = __builtin_fmaf(v[c][i], v[c][i], acc);
+            s[i] = acc;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s[i] = s[i] + nvr::xor_lane(s[i], 2);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s[i] = s[i] + nvr::xor_lane(s[i], 1);
+        float total = ((s[0] + s[4]) + (s[2] + s[6])) + ((s[1] + s[5]) + (s[3] + s[7]));
+        total = total + nvr::xor_lane(total, 16);
+        total = total + nvr::xor_lane(total, 8);
+        total = total + nvr::xor_lane(total, 4);
+        const float inv = nvr::inv_sqrt_rn(total / float(K) + eps);
+#pragma unroll
+        for (int c = 0; c < KC; ++c) {
+            float wf[8], o[8];
+            nvr::unpack8(*reinterpret_cast<const uint4*>(norm_weight + 256 * c + 8 * hm), wf);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = (v[c][i] * inv) * wf[i];
+            const uint4 ob = active ? nvr::pack8_split(o) : make_uint4(0, 0, 0, 0);
+            *reinterpret_cast<uint4*>(xs + row * LDX + 256 * c + 8 * hm) = ob;
+            if (writer && active) {
+                if (ADD && residual_out != nullptr)
+                    nvr::store_stream(residual_out + base + 256 * c, nvr::pack8_split(v[c]));
+                if (normed != nullptr) nvr::store_stream(normed + base + 256 * c, ob);
+            }
+        }
+    }
+    __syncthreads();
+
+    // 3. This wave's k quarter on MFMA.
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+        const int kk = kb + 32 * s + 8 * (lane / 16);
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const uint4 a = *reinterpret_cast<const uint4*>(xs + (t * 16 + lane % 16) * LDX + kk);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(wv[s]), acc[t], 0, 0, 0);
+        }
+    }
+
+    // 4. Sum the four quarters in wave order; lane l holds D[4 (l / 16) + r][l % 16].
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[(wave * MT + t) * 256 + (4 * (lane / 16) + r) * 16 + lane % 16] = acc[t][r];
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int i = threadIdx.x / 16, j = threadIdx.x % 16, row = t * 16 + i;
+        float sum = red[(0 * MT + t) * 256 + threadIdx.x];
+#pragma unroll
+        for (int q = 1; q < kWaves; ++q) sum += red[(q * MT + t) * 256 + threadIdx.x];
+        if (row < m) y[int64_t(row) * n + n0 + j] = nvr::f32_to_bf16(sum);
+    }
+}
+
+template <int KC, int MT, bool ADD>
+void launch(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_t* res_out, const uint16_t* nw,
+            const uint16_t* w, uint16_t* y, uint16_t* normed, int m, int n, float eps) {
+    constexpr int K = 256 * KC;
+    const size_t lds = sizeof(uint16_t) * MT * 16 * (K + kRowPad) + sizeof(float) * kWaves * MT * 256;
+    hipLaunchKernelGGL((rms_gemm<KC, MT, ADD>), dim3(unsigned(n / kTileN)), dim3(kThreads), lds, c->stream, x, res,
+                       res_out, nw, w, y, normed, m, n, eps);
+}
+
+template <int KC, bool ADD>
+void launch_rows(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_t* res_out, const uint16_t* nw,
+                 const uint16_t* w, uint16_t* y, uint16_t* normed, int m, int n, float eps) {
+    if (m <= 16) launch<KC, 1, ADD>(c, x, res, res_out, nw, w, y, normed, m, n, eps);
+    else launch<KC, 2, ADD>(c, x, res, res_out, nw, w, y, normed, m, n, eps);
+}
+
+}  // namespace
+
+extern "C" int nv_rms_gemm(nv_context* c, const void* x, const void* residual, void* residual_out,
+                           const void* norm_weight, const void* w, void* y, void* normed, int m, int n, int k,
+                           float eps) {
+    NVR_ACTIVATE(c);
+    if (m <= 0 || m > kMaxRows || n <= 0 || n % kTileN != 0)
+        return nvr::fail(-2, "rms_gemm: needs 1 <= m <= 32 rows and n a positive multiple of 16 (m %d, n %d)", m, n);
+    if (k != 512 && k != 1024 && k != 2048)
+        return nvr::fail(-2, "rms_gemm: k must be 512, 1024 or 2048 (k %d)", k);
+    if (residual == nullptr && residual_out != nullptr)
+        return nvr::fail(-2, "rms_gemm: residual_out needs a residual to add");
+    if (!nvr::aligned(x, 16) || !nvr::aligned(residual, 16) || !nvr::aligned(residual_out, 16) ||
+        !nvr::aligned(norm_weight, 16) || !nvr::aligned(w, 16) || !nvr::aligned(normed, 16))
+        return nvr::fail(-2, "rms_gemm: x, residual, residual_out, norm_weight, w and normed must be 16-byte aligned");
+    auto xb = static_cast<const uint16_t*>(x);
+    auto rb = static_cast<const uint16_t*>(residual);
+    auto ro = static_cast<uint16_t*>(residual_out);
+    auto nw = static_cast<const uint16_t*>(norm_weight);
+    auto wb = static_cast<const uint16_t*>(w);
+    auto yb = static_cast<uint16_t*>(y);
+    auto nb = static_cast<uint16_t*>(normed);
+    const bool add = residual != nullptr;
+    switch (k) {
+        case 512:
+            add ? launch_rows<2, true>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps)
+                : launch_rows<2, false>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps);
+            break;
+        case 1024:
+            add ? launch_rows<4, true>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps)
+                : launch_rows<4, false>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps);
+            break;
+        default:
+            add ? launch_rows<8, true>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps)
+                : launch_rows<8, false>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps);
+            break;
+    }
+    return nvr::launch_status();
+}

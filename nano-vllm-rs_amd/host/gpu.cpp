@@ -233,6 +233,10 @@ Graph Gpu::capture(const std::function<void()>& forward) const {
 }
 
 void Gpu::admit(const char* op, std::initializer_list<TensorArg> args) const {
+    admit(op, std::vector<TensorArg>(args));
+}
+
+void Gpu::admit(const char* op, const std::vector<TensorArg>& args) const {
     struct Span {
         const detail::Allocation* allocation;
         std::size_t begin, end;
@@ -301,6 +305,26 @@ void Gpu::add_rms_norm(const Buffer& x, const Buffer& residual, const Buffer& we
                            read_arg("weight", weight, 2, {hidden}), write_arg("out", out, 2, {rows, hidden})});
     require_status(nv_add_rms(context(), x.address(), residual.address(), weight.address(), out.address(),
                               as_dim(rows), as_dim(hidden), eps));
+}
+
+void Gpu::rms_gemm(const Buffer& x, const Buffer& residual, const Buffer& residual_out, const Buffer& norm_weight,
+                   const Buffer& w, const Buffer& y, const Buffer& normed, std::size_t m, std::size_t n,
+                   std::size_t k, float eps) const {
+    require_positive(eps, "rms_gemm eps");
+    if (residual.empty() && !residual_out.empty())
+        throw Error(Fault::Value, "rms_gemm: residual_out needs a residual to add");
+    if (m < 1 || m > 32 || n % 16 != 0 || (k != 512 && k != 1024 && k != 2048))
+        throw Error(Fault::Value, "rms_gemm: unsupported shape m " + std::to_string(m) + ", n " + std::to_string(n) +
+                                      ", k " + std::to_string(k));
+    std::vector<TensorArg> args = {read_arg("x", x, 2, {m, k}), read_arg("norm_weight", norm_weight, 2, {k}),
+                                   read_arg("w", w, 2, {n, k}), write_arg("y", y, 2, {m, n})};
+    if (!residual.empty()) args.push_back(read_arg("residual", residual, 2, {m, k}));
+    if (!residual_out.empty()) args.push_back(write_arg("residual_out", residual_out, 2, {m, k}));
+    if (!normed.empty()) args.push_back(write_arg("normed", normed, 2, {m, k}));
+    admit("rms_gemm", args);
+    auto ptr = [](const Buffer& b) { return b.empty() ? nullptr : b.address(); };
+    require_status(nv_rms_gemm(context(), x.address(), ptr(residual), ptr(residual_out), norm_weight.address(),
+                               w.address(), y.address(), ptr(normed), as_dim(m), as_dim(n), as_dim(k), eps));
 }
 
 void Gpu::add_rms_norm_gather(const Buffer& x, const Buffer& residual, const Buffer& weight, const Buffer& indices,

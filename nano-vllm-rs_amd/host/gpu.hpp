@@ -165,6 +165,7 @@ public:
     // Checks every tensor argument of kernel `op` (the contract above) and,
     // during a capture, records their allocations.
     void admit(const char* op, std::initializer_list<TensorArg> args) const;
+    void admit(const char* op, const std::vector<TensorArg>& args) const;
 
     // Y[m, n] = X[m, k] * W[n, k]^T, bf16 in/out, fp32 accumulation.
     void gemm(const Buffer& x, const Buffer& w, const Buffer& y, std::size_t m, std::size_t n, std::size_t k) const;
@@ -175,6 +176,12 @@ public:
     // residual <- bf16(x + residual); out <- RMSNorm(f32(x) + f32(residual)).
     void add_rms_norm(const Buffer& x, const Buffer& residual, const Buffer& weight, const Buffer& out,
                       std::size_t rows, std::size_t hidden, float eps) const;
+    // y = bf16(RMSNorm(x [+ residual]) W^T) for 1 <= m <= 32 rows (n % 16 == 0,
+    // k in {512, 1024, 2048}); residual_out <- bf16(x + residual) in another
+    // buffer and normed <- the normalised rows, each when not empty.
+    void rms_gemm(const Buffer& x, const Buffer& residual, const Buffer& residual_out, const Buffer& norm_weight,
+                  const Buffer& w, const Buffer& y, const Buffer& normed, std::size_t m, std::size_t n,
+                  std::size_t k, float eps) const;
     // add_rms_norm's output for input rows indices[r] in output row r (+0
     // rows for indices outside [0, input_rows)); residual is only read.
     void add_rms_norm_gather(const Buffer& x, const Buffer& residual, const Buffer& weight, const Buffer& indices,

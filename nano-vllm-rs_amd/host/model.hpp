@@ -56,7 +56,8 @@ struct ModelConfig {
 
 // Runtime capacities (src/model.rs:150-173; `graphs` is the reference's
 // cuda_graphs). fuse_decode_attention = false keeps every step on the
-// separate q/k norm + RoPE and attention launches.
+// separate q/k norm + RoPE and attention launches; fuse_norm_gemm = false
+// keeps the norms apart from the GEMMs that follow them.
 struct ModelOptions {
     int device = 0;
     std::size_t block_size = 256;
@@ -66,6 +67,7 @@ struct ModelOptions {
     std::size_t max_model_len = 4096;
     bool graphs = true;
     bool fuse_decode_attention = true;
+    bool fuse_norm_gemm = true;
 };
 
 // One scheduler step (src/runtime.rs:18-29): flattened rows, paged block
@@ -111,6 +113,7 @@ private:
 struct StepPlan {
     std::size_t rows = 0, sequences = 0, samples = 0;
     bool fused_attention = false;  // q/k norm + RoPE + KV write inside the attention launch
+    bool fused_norms = false;      // input / post-attention norms inside the qkv / gate_up GEMM launches
     bool replayable = false;       // served by a captured graph
 };
 
@@ -160,7 +163,9 @@ using StageObserver = std::function<void(Stage stage, std::size_t layer)>;
 struct Workspace {
     Buffer record, tokens, positions, sequence_ids, slots, tables, last_rows, temperatures, seeds;
     Buffer samples, partial_scores, partial_ids, rope_cache;
-    Buffer residual, hidden, normed, qkv, query, attention, gate_up, activated, gathered, logits;
+    // residual and residual_alt alternate as the residual stream when the
+    // norms run inside the GEMMs (QwenModel::residual() names the current one).
+    Buffer residual, residual_alt, hidden, normed, qkv, query, attention, gate_up, activated, gathered, logits;
 };
 struct LayerWeights {
     Buffer input_norm, qkv, q_norm, k_norm, o_proj, post_norm, gate_up, down, k_cache, v_cache;
@@ -185,6 +190,9 @@ public:
     const Buffer& embedding_weight() const { return embedding_; }
     const Buffer& final_norm_weight() const { return final_norm_; }
     std::size_t table_stride() const { return table_stride_; }
+    // The buffer holding the residual stream at the current point of the
+    // forward (for observers).
+    const Buffer& residual() const { return *residual_; }
 
     std::size_t graph_count() const { return graphs_.size(); }
     const ModelMemoryInfo& memory_usage() const { return memory_; }
@@ -212,6 +220,7 @@ private:
     std::map<std::pair<std::size_t, bool>, Graph> graphs_;  // (decode rows, fused attention) -> captured forward
     StageObserver observer_;
     bool capturing_ = false;
+    mutable const Buffer* residual_ = nullptr;
     std::size_t last_samples_ = 0;
 };
 

@@ -67,6 +67,7 @@ SIGNATURES = {
     "nv_rms": (_i, [_vp, _vp, _vp, _vp, _i, _i, _f]),
     "nv_add_rms": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _f]),
     "nv_add_rms_gather": (_i, [_vp] * 6 + [_i, _i, _i, _f]),
+    "nv_rms_gemm": (_i, [_vp] * 8 + [_i, _i, _i, _f]),
     "nv_qkv_rope": (_i, [_vp] * 9 + [_i] * 6 + [_f, _f]),
     "nv_rope_cache": (_i, [_vp, _vp, _i, _i, _f]),
     "nv_qkv_rope_cached": (_i, [_vp] * 9 + [_i] * 6 + [_f, _vp, _i]),
@@ -396,6 +397,29 @@ class Gpu:
         self._admit("add_rms_norm", [_r("x", x, 2, rows, hidden), _w("residual", residual, 2, rows, hidden),
                                      _r("weight", weight, 2, hidden), _w("out", out, 2, rows, hidden)])
         self._call(self.lib.nv_add_rms(self.handle, x.ptr, residual.ptr, weight.ptr, out.ptr, rows, hidden, eps))
+
+    RMS_GEMM_MAX_ROWS = 32
+
+    def rms_gemm(self, x: Buffer, residual: Buffer | None, residual_out: Buffer | None, norm_weight: Buffer,
+                 w: Buffer, y: Buffer, normed: Buffer | None, m: int, n: int, k: int, eps: float) -> None:
+        """y = bf16(RMSNorm(x [+ residual]) W^T) for 1 <= m <= 32 rows; residual_out <- bf16(x + residual)
+        (another buffer) and normed <- the normalised rows when given."""
+        require_positive(eps, "rms_gemm eps")
+        if residual is None and residual_out is not None:
+            raise ArgumentError("value", "rms_gemm: residual_out needs a residual to add")
+        if not 1 <= m <= self.RMS_GEMM_MAX_ROWS or n % 16 or k not in (512, 1024, 2048):
+            raise ArgumentError("value", f"rms_gemm: unsupported shape m {m}, n {n}, k {k}")
+        args = [_r("x", x, 2, m, k), _r("norm_weight", norm_weight, 2, k), _r("w", w, 2, n, k), _w("y", y, 2, m, n)]
+        if residual is not None:
+            args.append(_r("residual", residual, 2, m, k))
+        if residual_out is not None:
+            args.append(_w("residual_out", residual_out, 2, m, k))
+        if normed is not None:
+            args.append(_w("normed", normed, 2, m, k))
+        self._admit("rms_gemm", args)
+        ptr = lambda b: None if b is None else b.ptr  # noqa: E731
+        self._call(self.lib.nv_rms_gemm(self.handle, x.ptr, ptr(residual), ptr(residual_out), norm_weight.ptr, w.ptr,
+                                        y.ptr, ptr(normed), m, n, k, eps))
 
     def add_rms_norm_gather(self, x: Buffer, residual: Buffer, weight: Buffer, indices: Buffer, out: Buffer,
                             rows: int, hidden: int, input_rows: int, eps: float) -> None:

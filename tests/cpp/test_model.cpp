@@ -312,6 +312,25 @@ Mismatch compare(const std::vector<uint16_t>& got, const std::vector<uint16_t>& 
                                    std::to_string((got).size()) + " differ, first at " + std::to_string(m_.first)}; \
     } while (0)
 
+// A GEMM output against the float64 product of its own inputs: within
+// 2^-8 |y| + 2^-20 k sum|x w| (fp32 accumulation and one bf16 rounding).
+void check_gemm(const std::vector<uint16_t>& x, const std::vector<uint16_t>& w, const std::vector<uint16_t>& y,
+                std::size_t rows, std::size_t n, std::size_t k, const std::string& what) {
+    std::size_t outside = 0;
+    for (std::size_t r = 0; r < rows; ++r)
+        for (std::size_t j = 0; j < n; ++j) {
+            double acc = 0.0, mag = 0.0;
+            for (std::size_t i = 0; i < k; ++i) {
+                const double p = double(f32(x[r * k + i])) * double(f32(w[j * k + i]));
+                acc += p;
+                mag += std::fabs(p);
+            }
+            const double bound = 0x1.0p-8 * std::fabs(acc) + 0x1.0p-20 * double(k) * mag;
+            if (std::fabs(double(f32(y[r * n + j])) - acc) > bound) ++outside;
+        }
+    if (outside) throw harness::Failure{what + ": " + std::to_string(outside) + " outputs outside the GEMM bound"};
+}
+
 // Every stage of an eager forward against the oracle fed the GPU's own GEMM
 // outputs: the non-GEMM kernels must give the oracle's bits (SiLU within 1
 // bf16 ulp), the K/V caches must equal the oracle's, the lm_head GEMM must
@@ -359,7 +378,7 @@ struct OracleShadow {
         case Stage::Embedded:
             residual.resize(rows * c.hidden_size);
             ora_embedding(b.token_ids.data(), table.data(), residual.data(), R, H, int(c.vocab_size), int(threads));
-            CHECK_SAME(down16(w.residual, residual.size()), residual, 0, "embedding");
+            CHECK_SAME(down16(m.residual(), residual.size()), residual, 0, "embedding");
             break;
         case Stage::InputNorm:
             normed.resize(residual.size());
@@ -368,11 +387,14 @@ struct OracleShadow {
             else
                 ora_add_rms(hidden.data(), residual.data(), in_norm[l].data(), normed.data(), R, H, c.rms_norm_eps,
                             int(threads));
-            CHECK_SAME(down16(w.residual, residual.size()), residual, 0, at + "input norm residual");
+            CHECK_SAME(down16(m.residual(), residual.size()), residual, 0, at + "input norm residual");
             CHECK_SAME(down16(w.normed, normed.size()), normed, 0, at + "input norm");
             break;
         case Stage::Qkv:
             qkv = down16(w.qkv, rows * std::size_t(QH + 2 * KVH) * c.head_dim);
+            if (rows <= 16)  // decode-sized: the GEMM runs inside nv_rms_gemm
+                check_gemm(normed, down16(m.layer(l).qkv, std::size_t(QH + 2 * KVH) * D * c.hidden_size), qkv, rows,
+                           std::size_t(QH + 2 * KVH) * D, c.hidden_size, at + "qkv GEMM");
             break;
         case Stage::QkvRope:
         case Stage::Attention: {
@@ -412,7 +434,7 @@ struct OracleShadow {
         case Stage::PostNorm:
             ora_add_rms(hidden.data(), residual.data(), post_norm[l].data(), normed.data(), R, H, c.rms_norm_eps,
                         int(threads));
-            CHECK_SAME(down16(w.residual, residual.size()), residual, 0, at + "add-norm residual");
+            CHECK_SAME(down16(m.residual(), residual.size()), residual, 0, at + "add-norm residual");
             CHECK_SAME(down16(w.normed, normed.size()), normed, 0, at + "add-norm");
             break;
         case Stage::FinalNorm: {
@@ -427,11 +449,14 @@ struct OracleShadow {
             gathered.resize(n * c.hidden_size);
             ora_gather(normed.data(), b.last_token_indices.data(), gathered.data(), int(n), H, R, int(threads));
             CHECK_SAME(down16(w.gathered, gathered.size()), gathered, 0, "final norm of the sampled rows");
-            CHECK_SAME(down16(w.residual, before.size()), before, 0, "final norm residual");
+            CHECK_SAME(down16(m.residual(), before.size()), before, 0, "final norm residual");
             break;
         }
         case Stage::GateUp: {
             const std::vector<uint16_t> gate_up = down16(w.gate_up, rows * 2 * c.intermediate_size);
+            if (rows <= 16)
+                check_gemm(normed, down16(m.layer(l).gate_up, 2 * c.intermediate_size * c.hidden_size), gate_up,
+                           rows, 2 * c.intermediate_size, c.hidden_size, at + "gate_up GEMM");
             act.resize(rows * c.intermediate_size);
             ora_silu(gate_up.data(), act.data(), R, I, int(threads));
             break;

@@ -711,3 +711,52 @@ def test_gemm_few_rows_graph_replays(gpu):
         assert_bits_equal(replayed, down(y, np.uint16, (m, n)))
         want, bound = _gemm_bound(xa, wa)
         assert np.all(np.abs(f32_of(replayed).astype(np.float64) - want) <= bound)
+
+
+# ------------------------------------------------------- norm fused into GEMM --
+@pytest.mark.parametrize("m,n,k,add", [
+    (8, 4096, 1024, True),    # decode: post-attention norm + ... the qkv shape
+    (8, 6144, 1024, True),    # gate_up
+    (1, 4096, 1024, False),   # layer 0's plain RMSNorm, one row
+    (32, 4096, 1024, True),   # two row tiles
+    (17, 512, 2048, True),    # ragged second tile, k 2048
+    (5, 16, 512, False),      # one column tile, k 512
+])
+def test_rms_gemm_norm_bits_and_gemm_bound(gpu, m, n, k, add):
+    """nv_rms_gemm: the normalised rows and the updated residual equal the oracle's
+    (add-)RMSNorm bit for bit; y lies within the float64 GEMM bound of those rows
+    times W; a second launch gives the same bits."""
+    seed = m * 7 + n + k
+    xa = ora.normal_bf16((m, k), seed)
+    ra = ora.normal_bf16((m, k), seed + 1)
+    nw = ora.normal_bf16(k, seed + 2, 1.0, 0.02)
+    wa = ora.normal_bf16((n, k), seed + 3, 0.0, 0.05)
+    x, r, w = up(gpu, xa), up(gpu, ra), up(gpu, wa)
+    y, normed = gpu.alloc(m * n * 2), gpu.alloc(m * k * 2)
+    r_out = gpu.alloc(m * k * 2) if add else None
+    gpu.rms_gemm(x, r if add else None, r_out, up(gpu, nw), w, y, normed, m, n, k, EPS)
+    if add:
+        want_res, want_norm = ora.add_rms(xa, ra, nw, m, k, EPS)
+        assert_bits_equal(down(r_out, np.uint16, (m, k)), want_res, "residual_out")
+        assert_bits_equal(down(r, np.uint16, (m, k)), ra.reshape(m, k), "residual (read only)")
+    else:
+        want_norm = ora.rms(xa, nw, m, k, EPS)
+    assert_bits_equal(down(normed, np.uint16, (m, k)), want_norm, "normed")
+    first = down(y, np.uint16, (m, n)).copy()
+    want, bound = _gemm_bound(want_norm.reshape(m, k), wa)
+    got = f32_of(first).astype(np.float64)
+    assert np.all(np.abs(got - want) <= bound), np.max(np.abs(got - want) - bound)
+    gpu.rms_gemm(x, r if add else None, None, up(gpu, nw), w, y, None, m, n, k, EPS)
+    assert_bits_equal(down(y, np.uint16, (m, n)), first, "second launch")
+
+
+def test_rms_gemm_rejects_unsupported_shapes(gpu):
+    x, w, y = gpu.alloc(40 * 1024 * 2), gpu.alloc(4096 * 1024 * 2), gpu.alloc(40 * 4096 * 2)
+    nw = gpu.alloc(1024 * 2)
+    for m, n, k in ((33, 4096, 1024), (8, 4008, 1024), (8, 4096, 768)):
+        with pytest.raises(nvr.ArgumentError):
+            gpu.rms_gemm(x, None, None, nw, w, y, None, m, n, k, EPS)
+    lib, h = gpu.lib, gpu.handle
+    assert lib.nv_rms_gemm(h, x.ptr, None, None, nw.ptr, w.ptr, y.ptr, None, 33, 4096, 1024, EPS) == -2
+    assert lib.nv_rms_gemm(h, x.ptr, None, y.ptr, nw.ptr, w.ptr, y.ptr, None, 8, 4096, 1024, EPS) == -2
+    assert b"residual_out" in lib.nv_last_error()
