@@ -118,6 +118,18 @@ int nv_rms_gemm(nv_context* c, const void* x, const void* residual, void* residu
                 const void* norm_weight, const void* w, void* y, void* normed, int m, int n, int k,
                 float eps);
 
+/* nv_rms_gemm for the gate_up projection with SiLU·up (kernels/kernels.cu:356-365,
+ * nv_silu) as its epilogue: no single counterpart in the reference
+ * (src/model.rs:753-770). w_tiled is the [2 * intermediate, k] gate_up weight
+ * with its rows in tile order — tile t holds gate rows 8t..8t+7, then up rows
+ * 8t..8t+7 — and act[m, i] = bf16(silu(gate) * up) of the bf16-rounded GEMM
+ * outputs, with nv_silu's arithmetic (the same bits). gate_up (may be NULL)
+ * receives the GEMM output in the reference's [m, gate | up] layout.
+ * Limits as nv_rms_gemm, and intermediate a multiple of 8. */
+int nv_rms_gemm_silu(nv_context* c, const void* x, const void* residual, void* residual_out,
+                     const void* norm_weight, const void* w_tiled, void* gate_up, void* act, void* normed,
+                     int m, int intermediate, int k, float eps);
+
 /* kernels/kernels.cu:166-211,472 — per-head q/k RMSNorm, NeoX RoPE with the
  * angle computed inline, q -> qout, k/v -> paged caches at slots[r]
  * (src/gpu.rs:661-706). qkv is [rows, qh + 2*kvh, dim]; caches are

@@ -53,13 +53,18 @@ constexpr int kRowPad = 8;      // bf16 elements of padding per LDS row (spreads
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 // KC = k / 256 (16-byte chunks per lane of a half-wave row); MT = row tiles.
-template <int KC, int MT, bool ADD>
+// SILU: w is the gate_up weight with its rows in tile order (tile t = gate
+// rows 8t..8t+7, then up rows 8t..8t+7; n = 2 * inter), y (when not null)
+// receives gate_up in the reference's [gate | up] column order, and
+// act[m, 8t + j] = bf16(silu(gate) * up) of the tile's bf16 outputs.
+template <int KC, int MT, bool ADD, bool SILU>
 __global__ __launch_bounds__(kThreads) void rms_gemm(const uint16_t* __restrict__ x,
                                                      const uint16_t* __restrict__ residual,
                                                      uint16_t* __restrict__ residual_out,
                                                      const uint16_t* __restrict__ norm_weight,
                                                      const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
-                                                     uint16_t* __restrict__ normed, int m, int n, float eps) {
+                                                     uint16_t* __restrict__ normed, int m, int n, float eps,
+                                                     uint16_t* __restrict__ act, int inter) {
     constexpr int K = 256 * KC, KW = K / kWaves, STEPS = KW / 32, LDX = K + kRowPad;
     extern __shared__ __align__(16) unsigned char smem[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                          // [MT * 16][LDX]
@@ -188,34 +193,53 @@ __global__ __launch_bounds__(kThreads) void rms_gemm(const uint16_t* __restrict_
         float sum = red[(0 * MT + t) * 256 + threadIdx.x];
 #pragma unroll
         for (int q = 1; q < kWaves; ++q) sum += red[(q * MT + t) * 256 + threadIdx.x];
-        if (row < m) y[int64_t(row) * n + n0 + j] = nvr::f32_to_bf16(sum);
+        const uint16_t yb = nvr::f32_to_bf16(sum);
+        if constexpr (SILU) {
+            // Column j of tile b = blockIdx.x: gate index 8b + j (j < 8) or
+            // up index 8b + j - 8; lane j ^ 8 of the same 16-lane group
+            // holds the partner.
+            const int idx = 8 * int(blockIdx.x) + (j & 7);
+            const float own = nvr::bf16_to_f32(yb), partner = nvr::xor_lane(own, 8);
+            if (row < m) {
+                if (y != nullptr) y[int64_t(row) * n + (j < 8 ? idx : inter + idx)] = yb;
+                if (j < 8) act[int64_t(row) * inter + idx] = nvr::f32_to_bf16(nvr::silu_mul(own, partner));
+            }
+        } else {
+            if (row < m) y[int64_t(row) * n + n0 + j] = yb;
+        }
     }
 }
 
-template <int KC, int MT, bool ADD>
+template <int KC, int MT, bool ADD, bool SILU>
 void launch(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_t* res_out, const uint16_t* nw,
-            const uint16_t* w, uint16_t* y, uint16_t* normed, int m, int n, float eps) {
+            const uint16_t* w, uint16_t* y, uint16_t* normed, int m, int n, float eps, uint16_t* act) {
     constexpr int K = 256 * KC;
     const size_t lds = sizeof(uint16_t) * MT * 16 * (K + kRowPad) + sizeof(float) * kWaves * MT * 256;
-    hipLaunchKernelGGL((rms_gemm<KC, MT, ADD>), dim3(unsigned(n / kTileN)), dim3(kThreads), lds, c->stream, x, res,
-                       res_out, nw, w, y, normed, m, n, eps);
+    hipLaunchKernelGGL((rms_gemm<KC, MT, ADD, SILU>), dim3(unsigned(n / kTileN)), dim3(kThreads), lds, c->stream,
+                       x, res, res_out, nw, w, y, normed, m, n, eps, act, n / 2);
 }
 
-template <int KC, bool ADD>
+template <int KC, bool SILU>
 void launch_rows(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_t* res_out, const uint16_t* nw,
-                 const uint16_t* w, uint16_t* y, uint16_t* normed, int m, int n, float eps) {
-    if (m <= 16) launch<KC, 1, ADD>(c, x, res, res_out, nw, w, y, normed, m, n, eps);
-    else launch<KC, 2, ADD>(c, x, res, res_out, nw, w, y, normed, m, n, eps);
+                 const uint16_t* w, uint16_t* y, uint16_t* normed, int m, int n, float eps, uint16_t* act) {
+    const bool add = res != nullptr;
+    if (m <= 16) {
+        add ? launch<KC, 1, true, SILU>(c, x, res, res_out, nw, w, y, normed, m, n, eps, act)
+            : launch<KC, 1, false, SILU>(c, x, res, res_out, nw, w, y, normed, m, n, eps, act);
+    } else {
+        add ? launch<KC, 2, true, SILU>(c, x, res, res_out, nw, w, y, normed, m, n, eps, act)
+            : launch<KC, 2, false, SILU>(c, x, res, res_out, nw, w, y, normed, m, n, eps, act);
+    }
 }
 
-}  // namespace
-
-extern "C" int nv_rms_gemm(nv_context* c, const void* x, const void* residual, void* residual_out,
-                           const void* norm_weight, const void* w, void* y, void* normed, int m, int n, int k,
-                           float eps) {
+template <bool SILU>
+int launch_rms_gemm(nv_context* c, const void* x, const void* residual, void* residual_out, const void* norm_weight,
+                    const void* w, void* y, void* normed, int m, int n, int k, float eps, void* act) {
     NVR_ACTIVATE(c);
     if (m <= 0 || m > kMaxRows || n <= 0 || n % kTileN != 0)
         return nvr::fail(-2, "rms_gemm: needs 1 <= m <= 32 rows and n a positive multiple of 16 (m %d, n %d)", m, n);
+    if (SILU && act == nullptr) return nvr::fail(-2, "rms_gemm_silu: the activation output is required");
+    if (!SILU && y == nullptr) return nvr::fail(-2, "rms_gemm: the output y is required");
     if (k != 512 && k != 1024 && k != 2048)
         return nvr::fail(-2, "rms_gemm: k must be 512, 1024 or 2048 (k %d)", k);
     if (residual == nullptr && residual_out != nullptr)
@@ -230,20 +254,33 @@ extern "C" int nv_rms_gemm(nv_context* c, const void* x, const void* residual, v
     auto wb = static_cast<const uint16_t*>(w);
     auto yb = static_cast<uint16_t*>(y);
     auto nb = static_cast<uint16_t*>(normed);
-    const bool add = residual != nullptr;
+    auto ab = static_cast<uint16_t*>(act);
     switch (k) {
-        case 512:
-            add ? launch_rows<2, true>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps)
-                : launch_rows<2, false>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps);
-            break;
-        case 1024:
-            add ? launch_rows<4, true>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps)
-                : launch_rows<4, false>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps);
-            break;
-        default:
-            add ? launch_rows<8, true>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps)
-                : launch_rows<8, false>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps);
-            break;
+        case 512: launch_rows<2, SILU>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps, ab); break;
+        case 1024: launch_rows<4, SILU>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps, ab); break;
+        default: launch_rows<8, SILU>(c, xb, rb, ro, nw, wb, yb, nb, m, n, eps, ab); break;
     }
     return nvr::launch_status();
 }
+
+}  // namespace
+
+extern "C" {
+
+int nv_rms_gemm(nv_context* c, const void* x, const void* residual, void* residual_out, const void* norm_weight,
+                const void* w, void* y, void* normed, int m, int n, int k, float eps) {
+    return launch_rms_gemm<false>(c, x, residual, residual_out, norm_weight, w, y, normed, m, n, k, eps, nullptr);
+}
+
+int nv_rms_gemm_silu(nv_context* c, const void* x, const void* residual, void* residual_out,
+                     const void* norm_weight, const void* w_tiled, void* gate_up, void* act, void* normed, int m,
+                     int intermediate, int k, float eps) {
+    if (intermediate <= 0 || intermediate % 8 != 0) {
+        NVR_ACTIVATE(c);
+        return nvr::fail(-2, "rms_gemm_silu: intermediate must be a positive multiple of 8 (%d)", intermediate);
+    }
+    return launch_rms_gemm<true>(c, x, residual, residual_out, norm_weight, w_tiled, gate_up, normed, m,
+                                 2 * intermediate, k, eps, act);
+}
+
+}  // extern "C"

@@ -70,6 +70,17 @@ __device__ __forceinline__ void store_stream(void* p, const uint4& v) {
     __builtin_nontemporal_store(w, static_cast<u32x4_t*>(p));
 }
 
+// SiLU(g) * u for nv_silu and the SiLU epilogue of nv_rms_gemm_silu (one
+// definition, so both give the same bits): the hardware base-2 exponential and
+// reciprocal, with the IEEE division where 1 + exp(-g) >= 2^126 (there the
+// quotient is subnormal and the reciprocal would flush).
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896340736f);
+    const float d = 1.0f + e;
+    const float act = d < 0x1.0p126f ? g * __builtin_amdgcn_rcpf(d) : g / d;
+    return act * u;
+}
+
 // Round a float to bf16 precision and widen it back (the value a bf16 store
 // followed by a load would produce).
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }

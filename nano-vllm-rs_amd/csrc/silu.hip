@@ -22,12 +22,7 @@
 
 namespace {
 
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896340736f);
-    const float d = 1.0f + e;
-    const float act = d < 0x1.0p126f ? g * __builtin_amdgcn_rcpf(d) : g / d;
-    return act * u;
-}
+using nvr::silu_mul;
 
 // Eight elements on the reciprocal path, with one branch for the whole chunk
 // into the exact division (only taken when some gate is below about -87).

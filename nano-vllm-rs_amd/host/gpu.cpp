@@ -327,6 +327,43 @@ void Gpu::rms_gemm(const Buffer& x, const Buffer& residual, const Buffer& residu
                                w.address(), y.address(), ptr(normed), as_dim(m), as_dim(n), as_dim(k), eps));
 }
 
+void Gpu::rms_gemm_silu(const Buffer& x, const Buffer& residual, const Buffer& residual_out,
+                        const Buffer& norm_weight, const Buffer& w_tiled, const Buffer& gate_up, const Buffer& act,
+                        const Buffer& normed, std::size_t m, std::size_t intermediate, std::size_t k,
+                        float eps) const {
+    require_positive(eps, "rms_gemm_silu eps");
+    if (residual.empty() && !residual_out.empty())
+        throw Error(Fault::Value, "rms_gemm_silu: residual_out needs a residual to add");
+    if (m < 1 || m > 32 || intermediate % 8 != 0 || (k != 512 && k != 1024 && k != 2048))
+        throw Error(Fault::Value, "rms_gemm_silu: unsupported shape m " + std::to_string(m) + ", intermediate " +
+                                      std::to_string(intermediate) + ", k " + std::to_string(k));
+    std::vector<TensorArg> args = {read_arg("x", x, 2, {m, k}), read_arg("norm_weight", norm_weight, 2, {k}),
+                                   read_arg("w_tiled", w_tiled, 2, {2 * intermediate, k}),
+                                   write_arg("act", act, 2, {m, intermediate})};
+    if (!residual.empty()) args.push_back(read_arg("residual", residual, 2, {m, k}));
+    if (!residual_out.empty()) args.push_back(write_arg("residual_out", residual_out, 2, {m, k}));
+    if (!gate_up.empty()) args.push_back(write_arg("gate_up", gate_up, 2, {m, 2 * intermediate}));
+    if (!normed.empty()) args.push_back(write_arg("normed", normed, 2, {m, k}));
+    admit("rms_gemm_silu", args);
+    auto ptr = [](const Buffer& b) { return b.empty() ? nullptr : b.address(); };
+    require_status(nv_rms_gemm_silu(context(), x.address(), ptr(residual), ptr(residual_out), norm_weight.address(),
+                                    w_tiled.address(), ptr(gate_up), act.address(), ptr(normed), as_dim(m),
+                                    as_dim(intermediate), as_dim(k), eps));
+}
+
+std::vector<uint16_t> tile_gate_up_rows(const std::vector<uint16_t>& gate_up, std::size_t intermediate,
+                                        std::size_t k) {
+    if (intermediate % 8 != 0 || gate_up.size() != 2 * intermediate * k)
+        throw Error(Fault::Value, "tile_gate_up_rows: needs a [2 * intermediate, k] weight, intermediate % 8 == 0");
+    std::vector<uint16_t> out(gate_up.size());
+    for (std::size_t t = 0; t < intermediate / 8; ++t)
+        for (std::size_t half = 0; half < 2; ++half)
+            for (std::size_t e = 0; e < 8; ++e)
+                std::copy_n(gate_up.begin() + std::ptrdiff_t((half * intermediate + 8 * t + e) * k), k,
+                            out.begin() + std::ptrdiff_t((16 * t + 8 * half + e) * k));
+    return out;
+}
+
 void Gpu::add_rms_norm_gather(const Buffer& x, const Buffer& residual, const Buffer& weight, const Buffer& indices,
                               const Buffer& out, std::size_t rows, std::size_t hidden, std::size_t input_rows,
                               float eps) const {

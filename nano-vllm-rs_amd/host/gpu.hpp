@@ -70,6 +70,11 @@ void require_positive(float value, const char* what);
 // Fault::Value unless the head layout is one the kernels take (see above).
 void require_head_layout(std::size_t qheads, std::size_t kvheads, std::size_t head_dim);
 
+// The [2 * intermediate, k] gate_up weight (gate rows, then up rows) in the
+// tile row order rms_gemm_silu reads.
+std::vector<uint16_t> tile_gate_up_rows(const std::vector<uint16_t>& gate_up, std::size_t intermediate,
+                                        std::size_t k);
+
 namespace detail {
 struct Device;
 struct Allocation;
@@ -182,6 +187,13 @@ public:
     void rms_gemm(const Buffer& x, const Buffer& residual, const Buffer& residual_out, const Buffer& norm_weight,
                   const Buffer& w, const Buffer& y, const Buffer& normed, std::size_t m, std::size_t n,
                   std::size_t k, float eps) const;
+    // rms_gemm on the gate_up weight in tile row order (tile t: gate rows
+    // 8t..8t+7, then up rows 8t..8t+7; see tile_gate_up_rows) with SiLU·up as
+    // the epilogue: act <- silu(gate) * up; gate_up (when not empty) <- the
+    // GEMM output in [gate | up] order.
+    void rms_gemm_silu(const Buffer& x, const Buffer& residual, const Buffer& residual_out,
+                       const Buffer& norm_weight, const Buffer& w_tiled, const Buffer& gate_up, const Buffer& act,
+                       const Buffer& normed, std::size_t m, std::size_t intermediate, std::size_t k, float eps) const;
     // add_rms_norm's output for input rows indices[r] in output row r (+0
     // rows for indices outside [0, input_rows)); residual is only read.
     void add_rms_norm_gather(const Buffer& x, const Buffer& residual, const Buffer& weight, const Buffer& indices,

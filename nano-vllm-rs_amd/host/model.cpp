@@ -21,6 +21,15 @@ constexpr std::size_t kFusedNormRows = 16;
 
 std::string str(std::size_t v) { return std::to_string(v); }
 
+// Whether the model's shapes suit nv_rms_gemm / nv_rms_gemm_silu and the
+// options ask for them.
+bool norm_gemm_fits(const ModelConfig& c, const ModelOptions& o) {
+    const std::size_t h = c.hidden_size;
+    const std::size_t qkv_cols = (c.num_attention_heads + 2 * c.num_key_value_heads) * c.head_dim;
+    return o.fuse_norm_gemm && (h == 512 || h == 1024 || h == 2048) && qkv_cols % 16 == 0 &&
+           c.intermediate_size % 8 == 0;
+}
+
 [[noreturn]] void reject(Reject reason, const std::string& detail) {
     throw BatchError(reason, std::string("batch rejected (") + reject_name(reason) + "): " + detail);
 }
@@ -127,7 +136,7 @@ QwenModel::QwenModel(const ModelConfig& config, const ModelOptions& options, con
     const ModelConfig& c = config_;
     // Uploads the concatenation of the named tensors (fused projections
     // keep the reference's row order: q, k, v and gate, up).
-    auto upload = [&](const std::vector<std::pair<std::string, std::vector<std::size_t>>>& parts) {
+    auto read = [&](const std::vector<std::pair<std::string, std::vector<std::size_t>>>& parts) {
         std::vector<uint16_t> bits;
         for (const auto& [name, shape] : parts) {
             std::size_t n = 1;
@@ -137,10 +146,16 @@ QwenModel::QwenModel(const ModelConfig& config, const ModelOptions& options, con
                 throw Error(Fault::Extent, "weight " + name + ": " + str(t.size()) + " elements, shape holds " + str(n));
             bits.insert(bits.end(), t.begin(), t.end());
         }
+        return bits;
+    };
+    auto put = [&](const std::vector<uint16_t>& bits) {
         Buffer b = gpu_.alloc(bits.size() * 2);
         b.upload_u16(bits);
         memory_.weights_bytes += bits.size() * 2;
         return b;
+    };
+    auto upload = [&](const std::vector<std::pair<std::string, std::vector<std::size_t>>>& parts) {
+        return put(read(parts));
     };
     const std::size_t h = c.hidden_size, q = c.num_attention_heads * c.head_dim, kv = c.num_key_value_heads * c.head_dim;
     embedding_ = upload({{"model.embed_tokens.weight", {c.vocab_size, h}}});
@@ -159,8 +174,12 @@ QwenModel::QwenModel(const ModelConfig& config, const ModelOptions& options, con
         l.k_norm = upload({{p + "self_attn.k_norm.weight", {c.head_dim}}});
         l.o_proj = upload({{p + "self_attn.o_proj.weight", {h, q}}});
         l.post_norm = upload({{p + "post_attention_layernorm.weight", {h}}});
-        l.gate_up = upload({{p + "mlp.gate_proj.weight", {c.intermediate_size, h}},
-                            {p + "mlp.up_proj.weight", {c.intermediate_size, h}}});
+        const std::vector<uint16_t> gate_up = read({{p + "mlp.gate_proj.weight", {c.intermediate_size, h}},
+                                                    {p + "mlp.up_proj.weight", {c.intermediate_size, h}}});
+        l.gate_up = put(gate_up);
+        // The same weight in the tile row order of the fused gate_up + SiLU
+        // kernel (decode-sized steps).
+        if (norm_gemm_fits(c, o)) l.gate_up_tiled = put(tile_gate_up_rows(gate_up, c.intermediate_size, h));
         l.down = upload({{p + "mlp.down_proj.weight", {h, c.intermediate_size}}});
         l.k_cache = gpu_.alloc(cache_bytes);
         l.v_cache = gpu_.alloc(cache_bytes);
@@ -290,12 +309,9 @@ StepPlan QwenModel::plan(const Batch& b) const {
             }
         }
     }
-    // The fused norm + GEMM kernel serves up to 16 rows (beyond that every
+    // The fused norm + GEMM kernels serve up to 16 rows (beyond that every
     // block's copy of the norm costs more than the launch it saves).
-    const std::size_t h = config_.hidden_size;
-    const std::size_t qkv_cols = (config_.num_attention_heads + 2 * config_.num_key_value_heads) * config_.head_dim;
-    p.fused_norms = o.fuse_norm_gemm && p.rows <= kFusedNormRows && (h == 512 || h == 1024 || h == 2048) &&
-                    qkv_cols % 16 == 0 && (2 * config_.intermediate_size) % 16 == 0;
+    p.fused_norms = norm_gemm_fits(config_, o) && p.rows <= kFusedNormRows;
     p.replayable = o.graphs && b.is_decode && p.rows == p.sequences && p.samples == p.sequences;
     return p;
 }
@@ -366,18 +382,20 @@ void QwenModel::decoder_layer(const StepPlan& p, std::size_t i) const {
     gpu_.gemm(w.attention, l.o_proj, w.hidden, p.rows, h, q);
     observe(Stage::OutProj, i);
     if (p.fused_norms) {
+        // Post-attention add-norm, gate_up projection and SiLU·up in one launch.
         const Buffer* next = other(residual_);
-        gpu_.rms_gemm(w.hidden, *residual_, *next, l.post_norm, l.gate_up, w.gate_up, w.normed, p.rows,
-                      2 * c.intermediate_size, h, c.rms_norm_eps);
+        gpu_.rms_gemm_silu(w.hidden, *residual_, *next, l.post_norm, l.gate_up_tiled, w.gate_up, w.activated,
+                           w.normed, p.rows, c.intermediate_size, h, c.rms_norm_eps);
         residual_ = next;
         observe(Stage::PostNorm, i);
+        observe(Stage::GateUp, i);
     } else {
         gpu_.add_rms_norm(w.hidden, *residual_, l.post_norm, w.normed, p.rows, h, c.rms_norm_eps);
         observe(Stage::PostNorm, i);
         gpu_.gemm(w.normed, l.gate_up, w.gate_up, p.rows, 2 * c.intermediate_size, h);
+        observe(Stage::GateUp, i);
+        gpu_.silu_mul(w.gate_up, w.activated, p.rows, c.intermediate_size);
     }
-    observe(Stage::GateUp, i);
-    gpu_.silu_mul(w.gate_up, w.activated, p.rows, c.intermediate_size);
     observe(Stage::Activated, i);
     gpu_.gemm(w.activated, l.down, w.hidden, p.rows, h, c.intermediate_size);
     observe(Stage::Down, i);

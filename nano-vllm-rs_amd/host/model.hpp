@@ -150,7 +150,7 @@ enum class Stage {
     Attention,   // attention output (and the caches, in the fused form)
     OutProj,     // hidden = o-proj GEMM output
     PostNorm,    // residual and normed after the post-attention add-RMSNorm
-    GateUp,      // gate_up GEMM output
+    GateUp,      // gate_up GEMM output (with fused norms, seen after the SiLU too)
     Activated,   // SiLU(gate) * up
     Down,        // hidden = down GEMM output
     FinalNorm,   // gathered = the final add-RMSNorm of the sampled rows (residual not updated)
@@ -169,6 +169,7 @@ struct Workspace {
 };
 struct LayerWeights {
     Buffer input_norm, qkv, q_norm, k_norm, o_proj, post_norm, gate_up, down, k_cache, v_cache;
+    Buffer gate_up_tiled;  // gate_up in the fused SiLU kernel's tile row order (when fuse_norm_gemm)
 };
 
 class QwenModel {

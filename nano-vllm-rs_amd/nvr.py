@@ -68,6 +68,7 @@ SIGNATURES = {
     "nv_add_rms": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _f]),
     "nv_add_rms_gather": (_i, [_vp] * 6 + [_i, _i, _i, _f]),
     "nv_rms_gemm": (_i, [_vp] * 8 + [_i, _i, _i, _f]),
+    "nv_rms_gemm_silu": (_i, [_vp] * 9 + [_i, _i, _i, _f]),
     "nv_qkv_rope": (_i, [_vp] * 9 + [_i] * 6 + [_f, _f]),
     "nv_rope_cache": (_i, [_vp, _vp, _i, _i, _f]),
     "nv_qkv_rope_cached": (_i, [_vp] * 9 + [_i] * 6 + [_f, _vp, _i]),
@@ -133,6 +134,14 @@ def library(path: str | None = None) -> ctypes.CDLL:
     if path is None:
         _LIB = lib
     return lib
+
+
+def tile_gate_up_rows(gate_up: np.ndarray, intermediate: int) -> np.ndarray:
+    """The [2 * intermediate, k] gate_up weight (gate rows, then up rows) in the
+    tile row order nv_rms_gemm_silu reads: tile t = gate rows 8t..8t+7, then up
+    rows 8t..8t+7."""
+    w = np.asarray(gate_up).reshape(2, intermediate // 8, 8, -1)
+    return np.ascontiguousarray(w.transpose(1, 0, 2, 3).reshape(2 * intermediate, -1))
 
 
 def check_status(status: int, lib: ctypes.CDLL | None = None) -> None:
@@ -420,6 +429,29 @@ class Gpu:
         ptr = lambda b: None if b is None else b.ptr  # noqa: E731
         self._call(self.lib.nv_rms_gemm(self.handle, x.ptr, ptr(residual), ptr(residual_out), norm_weight.ptr, w.ptr,
                                         y.ptr, ptr(normed), m, n, k, eps))
+
+    def rms_gemm_silu(self, x: Buffer, residual: Buffer | None, residual_out: Buffer | None, norm_weight: Buffer,
+                      w_tiled: Buffer, gate_up: Buffer | None, act: Buffer, normed: Buffer | None, m: int,
+                      intermediate: int, k: int, eps: float) -> None:
+        """rms_gemm with SiLU·up as the epilogue: w_tiled is the gate_up weight in tile row order
+        (tile_gate_up_rows), act [m, intermediate] receives silu(gate) * up, gate_up (optional) the GEMM
+        output in [gate | up] order."""
+        require_positive(eps, "rms_gemm_silu eps")
+        if residual is None and residual_out is not None:
+            raise ArgumentError("value", "rms_gemm_silu: residual_out needs a residual to add")
+        if not 1 <= m <= self.RMS_GEMM_MAX_ROWS or intermediate % 8 or k not in (512, 1024, 2048):
+            raise ArgumentError("value", f"rms_gemm_silu: unsupported shape m {m}, intermediate {intermediate}, k {k}")
+        args = [_r("x", x, 2, m, k), _r("norm_weight", norm_weight, 2, k),
+                _r("w_tiled", w_tiled, 2, 2 * intermediate, k), _w("act", act, 2, m, intermediate)]
+        for name, buf, dims, writes in (("residual", residual, (m, k), False), ("residual_out", residual_out, (m, k), True),
+                                        ("gate_up", gate_up, (m, 2 * intermediate), True),
+                                        ("normed", normed, (m, k), True)):
+            if buf is not None:
+                args.append((_w if writes else _r)(name, buf, 2, *dims))
+        self._admit("rms_gemm_silu", args)
+        ptr = lambda b: None if b is None else b.ptr  # noqa: E731
+        self._call(self.lib.nv_rms_gemm_silu(self.handle, x.ptr, ptr(residual), ptr(residual_out), norm_weight.ptr,
+                                             w_tiled.ptr, ptr(gate_up), act.ptr, ptr(normed), m, intermediate, k, eps))
 
     def add_rms_norm_gather(self, x: Buffer, residual: Buffer, weight: Buffer, indices: Buffer, out: Buffer,
                             rows: int, hidden: int, input_rows: int, eps: float) -> None:

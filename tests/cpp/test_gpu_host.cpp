@@ -74,6 +74,20 @@ TEST(device_index_and_seed, "cpu") {
 }
 
 // -------------------------------------------------------------- GPU suite --
+TEST(tile_gate_up_rows_order, "cpu") {
+    const std::size_t inter = 24, k = 3;
+    std::vector<uint16_t> w(2 * inter * k);
+    for (std::size_t i = 0; i < w.size(); ++i) w[i] = uint16_t(i);
+    const std::vector<uint16_t> t = nvr::tile_gate_up_rows(w, inter, k);
+    for (std::size_t tile = 0; tile < inter / 8; ++tile)
+        for (std::size_t e = 0; e < 8; ++e)
+            for (std::size_t c = 0; c < k; ++c) {
+                CHECK(t[(16 * tile + e) * k + c] == w[(8 * tile + e) * k + c]);
+                CHECK(t[(16 * tile + 8 + e) * k + c] == w[(inter + 8 * tile + e) * k + c]);
+            }
+    CHECK_FAULT(nvr::tile_gate_up_rows(w, 20, k), nvr::Fault::Value);
+}
+
 TEST(gpu_views_keep_allocations_and_reject_overlap, "gpu") {  // src/gpu.rs:1169-1192
     nvr::Gpu gpu(0);
     nvr::Buffer packed = gpu.alloc(32);

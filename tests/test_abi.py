@@ -135,3 +135,14 @@ def test_bf16_helpers_round_trip():
     x = np.array([1.0, -2.5, 3.140625, 65536.0], np.float32)
     assert np.array_equal(nvr.bf16_values(nvr.bf16_bits(x)), x)
     assert nvr.bf16_bits(np.float32(1.0 + 2**-8)).item() == 0x3F80
+
+
+def test_tile_gate_up_rows_order():
+    """Tile t of the reordered weight holds gate rows 8t..8t+7, then up rows 8t..8t+7."""
+    inter, k = 24, 3
+    w = np.arange(2 * inter * k, dtype=np.uint16).reshape(2 * inter, k)
+    t = nvr.tile_gate_up_rows(w, inter)
+    for tile in range(inter // 8):
+        for e in range(8):
+            assert (t[16 * tile + e] == w[8 * tile + e]).all()
+            assert (t[16 * tile + 8 + e] == w[inter + 8 * tile + e]).all()

@@ -760,3 +760,37 @@ def test_rms_gemm_rejects_unsupported_shapes(gpu):
     assert lib.nv_rms_gemm(h, x.ptr, None, None, nw.ptr, w.ptr, y.ptr, None, 33, 4096, 1024, EPS) == -2
     assert lib.nv_rms_gemm(h, x.ptr, None, y.ptr, nw.ptr, w.ptr, y.ptr, None, 8, 4096, 1024, EPS) == -2
     assert b"residual_out" in lib.nv_last_error()
+
+
+@pytest.mark.parametrize("m,inter,k,add", [(8, 3072, 1024, True), (1, 3072, 1024, False), (20, 512, 2048, True),
+                                           (5, 64, 512, False)])
+def test_rms_gemm_silu_epilogue(gpu, m, inter, k, add):
+    """nv_rms_gemm_silu: the norm outputs are the oracle's bits; gate_up (written in
+    [gate | up] order from the tile-ordered weight) equals nv_rms_gemm's output with
+    the plain weight bit for bit and lies within the float64 GEMM bound; act equals
+    the oracle's SiLU·up of those gate_up values within 1 bf16 ulp."""
+    seed = m + inter + k
+    xa = ora.normal_bf16((m, k), seed)
+    ra = ora.normal_bf16((m, k), seed + 1)
+    nw = ora.normal_bf16(k, seed + 2, 1.0, 0.02)
+    wa = ora.normal_bf16((2 * inter, k), seed + 3, 0.0, 0.05)
+    x, r, nwb = up(gpu, xa), up(gpu, ra), up(gpu, nw)
+    tiled = up(gpu, nvr.tile_gate_up_rows(wa, inter))
+    gu, act, normed = gpu.alloc(m * 2 * inter * 2), gpu.alloc(m * inter * 2), gpu.alloc(m * k * 2)
+    r_out = gpu.alloc(m * k * 2) if add else None
+    gpu.rms_gemm_silu(x, r if add else None, r_out, nwb, tiled, gu, act, normed, m, inter, k, EPS)
+    if add:
+        want_res, want_norm = ora.add_rms(xa, ra, nw, m, k, EPS)
+        assert_bits_equal(down(r_out, np.uint16, (m, k)), want_res, "residual_out")
+    else:
+        want_norm = ora.rms(xa, nw, m, k, EPS)
+    assert_bits_equal(down(normed, np.uint16, (m, k)), want_norm, "normed")
+    got_gu = down(gu, np.uint16, (m, 2 * inter))
+    plain = gpu.alloc(m * 2 * inter * 2)
+    gpu.rms_gemm(x, r if add else None, None, nwb, up(gpu, wa), plain, None, m, 2 * inter, k, EPS)
+    assert_bits_equal(got_gu, down(plain, np.uint16, (m, 2 * inter)), "gate_up vs nv_rms_gemm")
+    want, bound = _gemm_bound(want_norm.reshape(m, k), wa)
+    assert np.all(np.abs(f32_of(got_gu).astype(np.float64) - want) <= bound)
+    want_act = ora.silu(got_gu.reshape(m, 2, inter), m, inter).reshape(m, inter)
+    assert bf16_ulp_diff(down(act, np.uint16, (m, inter)), want_act).max() <= 1
+
