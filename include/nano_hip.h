@@ -118,6 +118,13 @@ int nv_rms_gemm(nv_context* c, const void* x, const void* residual, void* residu
                 const void* norm_weight, const void* w, void* y, void* normed, int m, int n, int k,
                 float eps);
 
+/* nv_gemm for decode-sized batches without hipBLAS (kernels/kernels.cu:98-106's
+ * Y[m, n] = X[m, k] W[n, k]^T, bf16 in and out, fp32 accumulation on MFMA in a
+ * fixed order: equal to nv_gemm to fp32 rounding, the same bits on every
+ * launch). Limits (else -2): 1 <= m <= 32, n a multiple of 16,
+ * k in {1024, 2048, 3072, 4096}, 16-byte aligned x and w. */
+int nv_gemm_rows(nv_context* c, const void* x, const void* w, void* y, int m, int n, int k);
+
 /* nv_rms_gemm for the gate_up projection with SiLU·up (kernels/kernels.cu:356-365,
  * nv_silu) as its epilogue: no single counterpart in the reference
  * (src/model.rs:753-770). w_tiled is the [2 * intermediate, k] gate_up weight

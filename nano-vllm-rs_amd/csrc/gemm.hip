@@ -232,6 +232,63 @@ void launch_rows(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_t
     }
 }
 
+// Plain decode-sized GEMM (nv_gemm_rows): Y[m, n] = bf16(X W^T), m <= 32.
+// A block of WAVES waves owns a column tile of 16 and splits k over its
+// waves; each wave loads its W and X pieces straight into the MFMA operand
+// layouts (rows >= m read row m - 1 and are zeroed), all before the first
+// MFMA, and the partial tiles are summed through LDS in wave order. 16-wave
+// blocks serve narrow outputs (n = 1024: 64 blocks, each streaming its tile's
+// whole k with 16 waves of loads in flight), 4-wave blocks wide ones.
+template <int WAVES, int STEPS, int MT>
+__global__ __launch_bounds__(WAVES * 64) void gemm_rows(const uint16_t* __restrict__ x,
+                                                        const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
+                                                        int m, int n, int k) {
+    __shared__ float red[WAVES][MT][256];
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    const int n0 = blockIdx.x * kTileN;
+    const int kb = wave * (32 * STEPS) + 8 * (lane / 16);
+    uint4 wv[STEPS], xv[MT][STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) wv[s] = nvr::load_stream(w + int64_t(n0 + lane % 16) * k + kb + 32 * s);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int row = t * 16 + lane % 16;
+        const int64_t base = int64_t(row < m ? row : m - 1) * k + kb;
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const uint4 v = *reinterpret_cast<const uint4*>(x + base + 32 * s);
+            xv[t][s] = row < m ? v : make_uint4(0, 0, 0, 0);
+        }
+    }
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s)
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xv[t][s]), as_bf16x8(wv[s]), acc[t], 0, 0, 0);
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][t][(4 * (lane / 16) + r) * 16 + lane % 16] = acc[t][r];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < MT * 256; idx += WAVES * 64) {
+        const int t = idx / 256, e = idx % 256, row = t * 16 + e / 16;
+        float sum = red[0][t][e];
+#pragma unroll
+        for (int q = 1; q < WAVES; ++q) sum += red[q][t][e];
+        if (row < m) y[int64_t(row) * n + n0 + e % 16] = nvr::f32_to_bf16(sum);
+    }
+}
+
+template <int WAVES, int STEPS>
+void launch_rows_plain(nv_context* c, const uint16_t* x, const uint16_t* w, uint16_t* y, int m, int n, int k) {
+    const dim3 grid(unsigned(n / kTileN)), block(WAVES * 64);
+    if (m <= 16) hipLaunchKernelGGL((gemm_rows<WAVES, STEPS, 1>), grid, block, 0, c->stream, x, w, y, m, n, k);
+    else hipLaunchKernelGGL((gemm_rows<WAVES, STEPS, 2>), grid, block, 0, c->stream, x, w, y, m, n, k);
+}
+
 template <bool SILU>
 int launch_rms_gemm(nv_context* c, const void* x, const void* residual, void* residual_out, const void* norm_weight,
                     const void* w, void* y, void* normed, int m, int n, int k, float eps, void* act) {
@@ -270,6 +327,31 @@ extern "C" {
 int nv_rms_gemm(nv_context* c, const void* x, const void* residual, void* residual_out, const void* norm_weight,
                 const void* w, void* y, void* normed, int m, int n, int k, float eps) {
     return launch_rms_gemm<false>(c, x, residual, residual_out, norm_weight, w, y, normed, m, n, k, eps, nullptr);
+}
+
+int nv_gemm_rows(nv_context* c, const void* x, const void* w, void* y, int m, int n, int k) {
+    NVR_ACTIVATE(c);
+    if (m <= 0 || m > kMaxRows || n <= 0 || n % kTileN != 0)
+        return nvr::fail(-2, "gemm_rows: needs 1 <= m <= 32 rows and n a positive multiple of 16 (m %d, n %d)", m, n);
+    if (k != 1024 && k != 2048 && k != 3072 && k != 4096)
+        return nvr::fail(-2, "gemm_rows: k must be 1024, 2048, 3072 or 4096 (k %d)", k);
+    if (!nvr::aligned(x, 16) || !nvr::aligned(w, 16))
+        return nvr::fail(-2, "gemm_rows: x and w must be 16-byte aligned");
+    auto xb = static_cast<const uint16_t*>(x);
+    auto wb = static_cast<const uint16_t*>(w);
+    auto yb = static_cast<uint16_t*>(y);
+    if (n / kTileN >= 256 && k <= 2048) {  // enough tiles to fill the GPU with 4-wave blocks
+        if (k == 1024) launch_rows_plain<4, 8>(c, xb, wb, yb, m, n, k);
+        else launch_rows_plain<4, 16>(c, xb, wb, yb, m, n, k);
+    } else {
+        switch (k) {
+            case 1024: launch_rows_plain<16, 2>(c, xb, wb, yb, m, n, k); break;
+            case 2048: launch_rows_plain<16, 4>(c, xb, wb, yb, m, n, k); break;
+            case 3072: launch_rows_plain<16, 6>(c, xb, wb, yb, m, n, k); break;
+            default: launch_rows_plain<16, 8>(c, xb, wb, yb, m, n, k); break;
+        }
+    }
+    return nvr::launch_status();
 }
 
 int nv_rms_gemm_silu(nv_context* c, const void* x, const void* residual, void* residual_out,

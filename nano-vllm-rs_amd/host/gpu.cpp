@@ -307,6 +307,15 @@ void Gpu::add_rms_norm(const Buffer& x, const Buffer& residual, const Buffer& we
                               as_dim(rows), as_dim(hidden), eps));
 }
 
+void Gpu::gemm_rows(const Buffer& x, const Buffer& w, const Buffer& y, std::size_t m, std::size_t n,
+                    std::size_t k) const {
+    if (m < 1 || m > 32 || n % 16 != 0 || (k != 1024 && k != 2048 && k != 3072 && k != 4096))
+        throw Error(Fault::Value, "gemm_rows: unsupported shape m " + std::to_string(m) + ", n " + std::to_string(n) +
+                                      ", k " + std::to_string(k));
+    admit("gemm_rows", {read_arg("x", x, 2, {m, k}), read_arg("w", w, 2, {n, k}), write_arg("y", y, 2, {m, n})});
+    require_status(nv_gemm_rows(context(), x.address(), w.address(), y.address(), as_dim(m), as_dim(n), as_dim(k)));
+}
+
 void Gpu::rms_gemm(const Buffer& x, const Buffer& residual, const Buffer& residual_out, const Buffer& norm_weight,
                    const Buffer& w, const Buffer& y, const Buffer& normed, std::size_t m, std::size_t n,
                    std::size_t k, float eps) const {

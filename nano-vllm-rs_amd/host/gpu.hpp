@@ -181,6 +181,10 @@ public:
     // residual <- bf16(x + residual); out <- RMSNorm(f32(x) + f32(residual)).
     void add_rms_norm(const Buffer& x, const Buffer& residual, const Buffer& weight, const Buffer& out,
                       std::size_t rows, std::size_t hidden, float eps) const;
+    // Y[m, n] = X[m, k] * W[n, k]^T for 1 <= m <= 32 rows on this library's
+    // MFMA kernel (n % 16 == 0, k in {1024, 2048, 3072, 4096}).
+    void gemm_rows(const Buffer& x, const Buffer& w, const Buffer& y, std::size_t m, std::size_t n,
+                   std::size_t k) const;
     // y = bf16(RMSNorm(x [+ residual]) W^T) for 1 <= m <= 32 rows (n % 16 == 0,
     // k in {512, 1024, 2048}); residual_out <- bf16(x + residual) in another
     // buffer and normed <- the normalised rows, each when not empty.

@@ -68,6 +68,7 @@ SIGNATURES = {
     "nv_add_rms": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _f]),
     "nv_add_rms_gather": (_i, [_vp] * 6 + [_i, _i, _i, _f]),
     "nv_rms_gemm": (_i, [_vp] * 8 + [_i, _i, _i, _f]),
+    "nv_gemm_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i]),
     "nv_rms_gemm_silu": (_i, [_vp] * 9 + [_i, _i, _i, _f]),
     "nv_qkv_rope": (_i, [_vp] * 9 + [_i] * 6 + [_f, _f]),
     "nv_rope_cache": (_i, [_vp, _vp, _i, _i, _f]),
@@ -408,6 +409,13 @@ class Gpu:
         self._call(self.lib.nv_add_rms(self.handle, x.ptr, residual.ptr, weight.ptr, out.ptr, rows, hidden, eps))
 
     RMS_GEMM_MAX_ROWS = 32
+
+    def gemm_rows(self, x: Buffer, w: Buffer, y: Buffer, m: int, n: int, k: int) -> None:
+        """Y[m, n] = X[m, k] W[n, k]^T for 1 <= m <= 32 rows on this library's MFMA kernel."""
+        if not 1 <= m <= self.RMS_GEMM_MAX_ROWS or n % 16 or k not in (1024, 2048, 3072, 4096):
+            raise ArgumentError("value", f"gemm_rows: unsupported shape m {m}, n {n}, k {k}")
+        self._admit("gemm_rows", [_r("x", x, 2, m, k), _r("w", w, 2, n, k), _w("y", y, 2, m, n)])
+        self._call(self.lib.nv_gemm_rows(self.handle, x.ptr, w.ptr, y.ptr, m, n, k))
 
     def rms_gemm(self, x: Buffer, residual: Buffer | None, residual_out: Buffer | None, norm_weight: Buffer,
                  w: Buffer, y: Buffer, normed: Buffer | None, m: int, n: int, k: int, eps: float) -> None:

@@ -428,9 +428,18 @@ struct OracleShadow {
             break;
         }
         case Stage::OutProj:
-        case Stage::Down:
+        case Stage::Down: {
+            const std::vector<uint16_t> in = stage == Stage::OutProj
+                                                 ? down16(w.attention, rows * std::size_t(QH) * D)
+                                                 : down16(w.activated, rows * c.intermediate_size);
             hidden = down16(w.hidden, rows * c.hidden_size);
+            if (rows <= 16) {
+                const std::size_t k = stage == Stage::OutProj ? std::size_t(QH) * D : c.intermediate_size;
+                check_gemm(in, down16(stage == Stage::OutProj ? m.layer(l).o_proj : m.layer(l).down, c.hidden_size * k),
+                           hidden, rows, c.hidden_size, k, at + (stage == Stage::OutProj ? "o_proj GEMM" : "down GEMM"));
+            }
             break;
+        }
         case Stage::PostNorm:
             ora_add_rms(hidden.data(), residual.data(), post_norm[l].data(), normed.data(), R, H, c.rms_norm_eps,
                         int(threads));

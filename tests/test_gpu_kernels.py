@@ -794,3 +794,27 @@ def test_rms_gemm_silu_epilogue(gpu, m, inter, k, add):
     want_act = ora.silu(got_gu.reshape(m, 2, inter), m, inter).reshape(m, inter)
     assert bf16_ulp_diff(down(act, np.uint16, (m, inter)), want_act).max() <= 1
 
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 1024, 2048), (8, 1024, 3072), (8, 151936, 1024), (1, 4096, 1024),
+                                   (16, 1024, 2048), (32, 1024, 3072), (17, 2048, 4096), (3, 16, 1024)])
+def test_gemm_rows_within_bound_and_deterministic(gpu, m, n, k):
+    """nv_gemm_rows against the float64 product (the bound of nv_gemm's test); a
+    second launch and a graph replay give the same bits."""
+    seed = m * 3 + n + k
+    xa = ora.normal_bf16((m, k), seed)
+    wa = ora.normal_bf16((n, k), seed + 1, 0.0, 0.05)
+    x, w, y = up(gpu, xa), up(gpu, wa), gpu.alloc(m * n * 2)
+    gpu.gemm_rows(x, w, y, m, n, k)
+    first = down(y, np.uint16, (m, n)).copy()
+    if n * k <= 4096 * 4096:
+        want, bound = _gemm_bound(xa, wa)
+        assert np.all(np.abs(f32_of(first).astype(np.float64) - want) <= bound)
+    else:  # the vocabulary-wide shape: 4096 columns spread over the output
+        cols = np.random.default_rng(seed).choice(n, 4096, replace=False)
+        want, bound = _gemm_bound(xa, wa[cols])
+        assert np.all(np.abs(f32_of(first[:, cols]).astype(np.float64) - want) <= bound)
+    gpu.sync()
+    graph = gpu.capture(lambda: gpu.gemm_rows(x, w, y, m, n, k))
+    graph.replay()
+    assert_bits_equal(down(y, np.uint16, (m, n)), first, "graph replay")
