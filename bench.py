@@ -257,7 +257,7 @@ def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=()):
     w = fill.normal(H * 2, 1.0, 0.02)
     # A plain device-to-device copy of 256 MiB by the HIP runtime's own copy
     # kernel: the counters' calibration and the copy rate of this GPU.
-    if want(COPY_CASE):
+    if COPY_CASE in only:  # the counters' calibration: only when named
         n = COPY_BYTES
         srcs = [gpu.alloc(n) for _ in range(3)]
         dsts = [gpu.alloc(n) for _ in range(3)]
