@@ -12,24 +12,25 @@
 // (~3.5 us) and the GEMM that follows streams its weights in a few us; fusing
 // them removes a launch and overlaps the norm with the weight stream.
 //
-// Layout (256 threads, column tile of 16 outputs per block, n / 16 blocks):
+// Layout (W = 4 or 8 waves, column tile of 16 outputs per block, n / 16
+// blocks):
 //  1. Each half-wave issues the loads of its first input row (x, residual),
 //     then every wave its share of the tile's weights: wave w owns the k range
-//     [w k/4, (w+1) k/4) and lane l loads, for each 32-wide k step, the 16
+//     [w k/W, (w+1) k/W) and lane l loads, for each 32-wide k step, the 16
 //     bytes W[n0 + l % 16][k0 + 8 (l / 16) ..] — the B operand layout of
 //     v_mfma_f32_16x16x32_bf16 (B[k][j] with k = 8 (l / 16) + e, j = l % 16).
 //     Loads retire in issue order, so the norm waits only for its rows.
 //  2. While the weights stream in, the block normalises the m input rows (one
-//     row per half-wave per pass of 8 rows, the layout and reduction tree of
+//     row per half-wave per pass of 2W rows, the layout and reduction tree of
 //     norm.hip's rms_rows_fast) into an LDS tile X[16 or 32][k] (rows >= m
 //     zero). Block 0 also writes residual_out (bf16(x + residual)) and, when
 //     asked, the normalised rows.
 //  3. Each wave runs its k steps on MFMA: A = X[l % 16 (+16)][k0 + 8 (l / 16) ..]
 //     from LDS, one accumulator tile per 16 rows.
-//  4. The four waves' partial tiles are summed through LDS in wave order and
+//  4. The W waves' partial tiles are summed through LDS in wave order and
 //     rounded once to bf16.
-// The GEMM's summation order (MFMA's, then the four k quarters in order) is
-// fixed, so every launch gives the same bits; it is not hipBLAS's order, so
+// The GEMM's summation order (MFMA's, then the W k slices in order, W fixed
+// by n) is fixed, so every launch of a shape gives the same bits; it is not hipBLAS's order, so
 // the result matches nv_gemm's to fp32 rounding (checked against the float64
 // product's bound), while the norm outputs match the oracle bit for bit.
 // The residual is read from one buffer and written to another: a block that
@@ -45,7 +46,6 @@ using nvr::kWave;
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256, kWaves = kThreads / kWave;
 constexpr int kTileN = 16;      // output columns per block (MFMA N)
 constexpr int kMaxRows = 32;    // two MFMA row tiles
 constexpr int kRowPad = 8;      // bf16 elements of padding per LDS row (spreads the A reads over the banks)
@@ -57,18 +57,18 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin
 // rows 8t..8t+7, then up rows 8t..8t+7; n = 2 * inter), y (when not null)
 // receives gate_up in the reference's [gate | up] column order, and
 // act[m, 8t + j] = bf16(silu(gate) * up) of the tile's bf16 outputs.
-template <int KC, int MT, bool ADD, bool SILU>
-__global__ __launch_bounds__(kThreads) void rms_gemm(const uint16_t* __restrict__ x,
+template <int KC, int MT, bool ADD, bool SILU, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void rms_gemm(const uint16_t* __restrict__ x,
                                                      const uint16_t* __restrict__ residual,
                                                      uint16_t* __restrict__ residual_out,
                                                      const uint16_t* __restrict__ norm_weight,
                                                      const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
                                                      uint16_t* __restrict__ normed, int m, int n, float eps,
                                                      uint16_t* __restrict__ act, int inter) {
-    constexpr int K = 256 * KC, KW = K / kWaves, STEPS = KW / 32, LDX = K + kRowPad;
+    constexpr int K = 256 * KC, KW = K / WAVES, STEPS = KW / 32, LDX = K + kRowPad, ROWS = 2 * WAVES;
     extern __shared__ __align__(16) unsigned char smem[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(smem);                          // [MT * 16][LDX]
-    float* red = reinterpret_cast<float*>(smem + sizeof(uint16_t) * MT * 16 * LDX);  // [kWaves][MT][256]
+    float* red = reinterpret_cast<float*>(smem + sizeof(uint16_t) * MT * 16 * LDX);  // [WAVES][MT][256]
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
     const int n0 = blockIdx.x * kTileN;
 
@@ -77,8 +77,8 @@ __global__ __launch_bounds__(kThreads) void rms_gemm(const uint16_t* __restrict_
     // issued first) overlaps the weight stream.
     const int half = lane >> 5, hm = lane & 31;
     const bool writer = blockIdx.x == 0;
-    const int passes = (m + 7) / 8;  // uniform; rows of a pass: pass * 8 + (wave * 2 + half)
-    auto row_of = [&](int pass) { return pass * 8 + wave * 2 + half; };
+    const int passes = (m + ROWS - 1) / ROWS;  // uniform; rows of a pass: pass * ROWS + (wave * 2 + half)
+    auto row_of = [&](int pass) { return pass * ROWS + wave * 2 + half; };
     auto base_of = [&](int pass) { return int64_t(row_of(pass) < m ? row_of(pass) : 0) * K + 8 * hm; };
     uint4 xw[KC], rw[KC];
 #pragma unroll
@@ -95,14 +95,14 @@ __global__ __launch_bounds__(kThreads) void rms_gemm(const uint16_t* __restrict_
 
     // 2. The norm of every input row into LDS (rms_rows_fast's arithmetic);
     // row tiles past the last pass are zero.
-    if (passes < MT * 2) {
-        for (int i = threadIdx.x; i < (MT * 2 - passes) * 8 * (K / 8); i += kThreads) {
-            const int row = passes * 8 + i / (K / 8), col = 8 * (i % (K / 8));
+    if (passes * ROWS < MT * 16) {
+        for (int i = threadIdx.x; i < (MT * 16 - passes * ROWS) * (K / 8); i += WAVES * 64) {
+            const int row = passes * ROWS + i / (K / 8), col = 8 * (i % (K / 8));
             *reinterpret_cast<uint4*>(xs + row * LDX + col) = make_uint4(0, 0, 0, 0);
         }
     }
 #pragma unroll
-    for (int pass = 0; pass < MT * 2; ++pass) {
+    for (int pass = 0; pass < (MT * 16 + ROWS - 1) / ROWS; ++pass) {
         if (pass >= passes) break;  // uniform
         const int row = row_of(pass);
         const bool active = row < m;
@@ -187,12 +187,13 @@ __global__ __launch_bounds__(kThreads) void rms_gemm(const uint16_t* __restrict_
 #pragma unroll
         for (int r = 0; r < 4; ++r) red[(wave * MT + t) * 256 + (4 * (lane / 16) + r) * 16 + lane % 16] = acc[t][r];
     __syncthreads();
+    // Output (t, e): tile t, element e = 16 i + j; wave-uniform trip count.
+    for (int idx = threadIdx.x; idx < MT * 256; idx += WAVES * 64) {
+        const int t = idx / 256, e = idx % 256;
+        const int i = e / 16, j = e % 16, row = t * 16 + i;
+        float sum = red[(0 * MT + t) * 256 + e];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-        const int i = threadIdx.x / 16, j = threadIdx.x % 16, row = t * 16 + i;
-        float sum = red[(0 * MT + t) * 256 + threadIdx.x];
-#pragma unroll
-        for (int q = 1; q < kWaves; ++q) sum += red[(q * MT + t) * 256 + threadIdx.x];
+        for (int q = 1; q < WAVES; ++q) sum += red[(q * MT + t) * 256 + e];
         const uint16_t yb = nvr::f32_to_bf16(sum);
         if constexpr (SILU) {
             // Column j of tile b = blockIdx.x: gate index 8b + j (j < 8) or
@@ -210,13 +211,26 @@ __global__ __launch_bounds__(kThreads) void rms_gemm(const uint16_t* __restrict_
     }
 }
 
+// Blocks of 8 waves when the grid is at most one block per CU (n <= 4096:
+// more loads in flight per CU, and for 32 rows two passes of the norm
+// instead of four); 4 waves when it is wider, where two smaller blocks per
+// CU (LDS permitting) hide each other's norm.
+constexpr int kCus = 256;
+
+template <int KC, int MT, bool ADD, bool SILU, int WAVES>
+void launch_waves(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_t* res_out, const uint16_t* nw,
+                  const uint16_t* w, uint16_t* y, uint16_t* normed, int m, int n, float eps, uint16_t* act) {
+    constexpr int K = 256 * KC;
+    const size_t lds = sizeof(uint16_t) * MT * 16 * (K + kRowPad) + sizeof(float) * WAVES * MT * 256;
+    hipLaunchKernelGGL((rms_gemm<KC, MT, ADD, SILU, WAVES>), dim3(unsigned(n / kTileN)), dim3(WAVES * 64), lds,
+                       c->stream, x, res, res_out, nw, w, y, normed, m, n, eps, act, n / 2);
+}
+
 template <int KC, int MT, bool ADD, bool SILU>
 void launch(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_t* res_out, const uint16_t* nw,
             const uint16_t* w, uint16_t* y, uint16_t* normed, int m, int n, float eps, uint16_t* act) {
-    constexpr int K = 256 * KC;
-    const size_t lds = sizeof(uint16_t) * MT * 16 * (K + kRowPad) + sizeof(float) * kWaves * MT * 256;
-    hipLaunchKernelGGL((rms_gemm<KC, MT, ADD, SILU>), dim3(unsigned(n / kTileN)), dim3(kThreads), lds, c->stream,
-                       x, res, res_out, nw, w, y, normed, m, n, eps, act, n / 2);
+    if (n / kTileN <= kCus) launch_waves<KC, MT, ADD, SILU, 8>(c, x, res, res_out, nw, w, y, normed, m, n, eps, act);
+    else launch_waves<KC, MT, ADD, SILU, 4>(c, x, res, res_out, nw, w, y, normed, m, n, eps, act);
 }
 
 template <int KC, bool SILU>
