@@ -119,9 +119,10 @@ int nv_rms_gemm(nv_context* c, const void* x, const void* residual, void* residu
                 float eps);
 
 /* nv_gemm for decode-sized batches without hipBLAS (kernels/kernels.cu:98-106's
- * Y[m, n] = X[m, k] W[n, k]^T, bf16 in and out, fp32 accumulation on MFMA in a
- * fixed order: equal to nv_gemm to fp32 rounding, the same bits on every
- * launch). Limits (else -2): 1 <= m <= 32, n a multiple of 16,
+ * Y[m, n] = X[m, k] W[n, k]^T, bf16 in and out, fp32 accumulation in a fixed
+ * order — on MFMA, or with dot2 instructions for outputs narrower than one
+ * 16-column tile per CU at m <= 16: equal to nv_gemm to fp32 rounding, the
+ * same bits on every launch of a shape). Limits (else -2): 1 <= m <= 32, n a multiple of 16,
  * k in {1024, 2048, 3072, 4096}, 16-byte aligned x and w. */
 int nv_gemm_rows(nv_context* c, const void* x, const void* w, void* y, int m, int n, int k);
 

@@ -250,9 +250,10 @@ void launch_rows(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_t
 // A block of WAVES waves owns a column tile of 16 and splits k over its
 // waves; each wave loads its W and X pieces straight into the MFMA operand
 // layouts (rows >= m read row m - 1 and are zeroed), all before the first
-// MFMA, and the partial tiles are summed through LDS in wave order. 16-wave
-// blocks serve narrow outputs (n = 1024: 64 blocks, each streaming its tile's
-// whole k with 16 waves of loads in flight), 4-wave blocks wide ones.
+// MFMA, and the partial tiles are summed through LDS in wave order. 4-wave
+// blocks serve wide outputs; outputs with fewer 16-column tiles than CUs take
+// gemm_narrow below 17 rows and 16-wave blocks (each streaming its tile's
+// whole k with 16 waves of loads in flight) from 17 rows.
 template <int WAVES, int STEPS, int MT>
 __global__ __launch_bounds__(WAVES * 64) void gemm_rows(const uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
@@ -293,6 +294,72 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_rows(const uint16_t* __restri
 #pragma unroll
         for (int q = 1; q < WAVES; ++q) sum += red[q][t][e];
         if (row < m) y[int64_t(row) * n + n0 + e % 16] = nvr::f32_to_bf16(sum);
+    }
+}
+
+// Narrow decode GEMM (nv_gemm_rows when n / 16 column tiles leave most CUs
+// idle, as n = 1024 does with 64): one block per NC = 32 / MR output columns
+// (n = 1024: 256 blocks at m <= 8, 512 at m <= 16) and one thread per
+// 16-byte chunk of k (THREADS = k / 8). A thread loads its chunk of the NC
+// weight rows and of the MR input rows (rows >= m repeat row m - 1 and are
+// never written), forms the MR * NC partial dot products in k order with
+// v_dot2_f32_bf16 (four per chunk), and stores them to LDS. Then FIN threads
+// per output sum the partials of chunks p, p + FIN, ... in order and fold
+// across their FIN lanes with DPP (lane ^ 1, lane ^ 2, then the other half of
+// the 8-lane group). The order is fixed, so every launch gives the same bits.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+template <int MR, int THREADS>
+__global__ __launch_bounds__(THREADS) void gemm_narrow(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                       uint16_t* __restrict__ y, int m, int n, int k) {
+    constexpr int NC = 32 / MR, OUT = 32, FIN = THREADS >= 256 ? 8 : 4, PER = THREADS / FIN;
+    constexpr int LDP = THREADS + 8;  // row pitch: the 8 outputs a wave folds start in different banks
+    static_assert(OUT * FIN <= THREADS && THREADS % 64 == 0, "gemm_narrow block shape");
+    __shared__ float part[OUT * LDP];
+    const int t = threadIdx.x;
+    const int c0 = blockIdx.x * NC;
+    uint4 wv[NC], xv[MR];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) wv[c] = nvr::load_stream(w + int64_t(c0 + c) * k + 8 * t);
+#pragma unroll
+    for (int r = 0; r < MR; ++r) xv[r] = *reinterpret_cast<const uint4*>(x + int64_t(r < m ? r : m - 1) * k + 8 * t);
+#pragma unroll
+    for (int r = 0; r < MR; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            float acc = dot2(xv[r].x, wv[c].x, 0.0f);
+            acc = dot2(xv[r].y, wv[c].y, acc);
+            acc = dot2(xv[r].z, wv[c].z, acc);
+            acc = dot2(xv[r].w, wv[c].w, acc);
+            part[(r * NC + c) * LDP + t] = acc;
+        }
+    __syncthreads();
+    if (t < OUT * FIN) {
+        const int o = t / FIN, p = t % FIN;
+        const float* src = part + o * LDP + p;
+        float s = src[0];
+#pragma unroll
+        for (int i = 1; i < PER; ++i) s += src[i * FIN];
+        s += nvr::dpp<nvr::kDppQuadXor1>(s);
+        s += nvr::dpp<nvr::kDppQuadXor2>(s);
+        if constexpr (FIN == 8) s += nvr::dpp<nvr::kDppRowHalfMirror>(s);
+        const int r = o / NC;
+        if (p == 0 && r < m) y[int64_t(r) * n + c0 + o % NC] = nvr::f32_to_bf16(s);
+    }
+}
+
+template <int MR>
+void launch_narrow(nv_context* c, const uint16_t* x, const uint16_t* w, uint16_t* y, int m, int n, int k) {
+    const dim3 grid(unsigned(n / (32 / MR)));
+    switch (k) {
+        case 1024: hipLaunchKernelGGL((gemm_narrow<MR, 128>), grid, dim3(128), 0, c->stream, x, w, y, m, n, k); break;
+        case 2048: hipLaunchKernelGGL((gemm_narrow<MR, 256>), grid, dim3(256), 0, c->stream, x, w, y, m, n, k); break;
+        case 3072: hipLaunchKernelGGL((gemm_narrow<MR, 384>), grid, dim3(384), 0, c->stream, x, w, y, m, n, k); break;
+        default: hipLaunchKernelGGL((gemm_narrow<MR, 512>), grid, dim3(512), 0, c->stream, x, w, y, m, n, k); break;
     }
 }
 
@@ -354,7 +421,10 @@ int nv_gemm_rows(nv_context* c, const void* x, const void* w, void* y, int m, in
     auto xb = static_cast<const uint16_t*>(x);
     auto wb = static_cast<const uint16_t*>(w);
     auto yb = static_cast<uint16_t*>(y);
-    if (n / kTileN >= 256 && k <= 2048) {  // enough tiles to fill the GPU with 4-wave blocks
+    if (n / kTileN < 256 && m <= 16) {  // too few 16-column tiles to fill the GPU
+        if (m <= 8) launch_narrow<8>(c, xb, wb, yb, m, n, k);
+        else launch_narrow<16>(c, xb, wb, yb, m, n, k);
+    } else if (n / kTileN >= 256 && k <= 2048) {  // enough tiles to fill the GPU with 4-wave blocks
         if (k == 1024) launch_rows_plain<4, 8>(c, xb, wb, yb, m, n, k);
         else launch_rows_plain<4, 16>(c, xb, wb, yb, m, n, k);
     } else {

@@ -379,9 +379,13 @@ void QwenModel::decoder_layer(const StepPlan& p, std::size_t i) const {
                              table_stride_, p.sequences, o.max_model_len);
     }
     observe(Stage::Attention, i);
-    // Decode-sized batches take this library's MFMA kernel for the output
-    // projection (measured 5.2 vs 5.5 us at 8 rows, 6.0 vs 6.3 at 16).
-    if (p.fused_norms && (q == 1024 || q == 2048 || q == 3072 || q == 4096) && h % 16 == 0)
+    // Decode-sized batches take nv_gemm_rows for the output and down
+    // projections (hidden 1024 at 8 rows: 3.4 vs 5.5 us for o_proj, 4.2 vs
+    // 7.2 us for down against hipBLAS).
+    auto rows_gemm = [&](std::size_t k) {
+        return p.fused_norms && (k == 1024 || k == 2048 || k == 3072 || k == 4096) && h % 16 == 0;
+    };
+    if (rows_gemm(q))
         gpu_.gemm_rows(w.attention, l.o_proj, w.hidden, p.rows, h, q);
     else
         gpu_.gemm(w.attention, l.o_proj, w.hidden, p.rows, h, q);
@@ -402,7 +406,10 @@ void QwenModel::decoder_layer(const StepPlan& p, std::size_t i) const {
         gpu_.silu_mul(w.gate_up, w.activated, p.rows, c.intermediate_size);
     }
     observe(Stage::Activated, i);
-    gpu_.gemm(w.activated, l.down, w.hidden, p.rows, h, c.intermediate_size);
+    if (rows_gemm(c.intermediate_size))
+        gpu_.gemm_rows(w.activated, l.down, w.hidden, p.rows, h, c.intermediate_size);
+    else
+        gpu_.gemm(w.activated, l.down, w.hidden, p.rows, h, c.intermediate_size);
     observe(Stage::Down, i);
 }
 

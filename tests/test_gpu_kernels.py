@@ -797,7 +797,8 @@ def test_rms_gemm_silu_epilogue(gpu, m, inter, k, add):
 
 
 @pytest.mark.parametrize("m,n,k", [(8, 1024, 2048), (8, 1024, 3072), (8, 151936, 1024), (1, 4096, 1024),
-                                   (16, 1024, 2048), (32, 1024, 3072), (17, 2048, 4096), (3, 16, 1024)])
+                                   (16, 1024, 2048), (32, 1024, 3072), (17, 2048, 4096), (3, 16, 1024),
+                                   (1, 1024, 1024), (12, 1024, 4096), (9, 2032, 3072), (5, 4096, 4096)])
 def test_gemm_rows_within_bound_and_deterministic(gpu, m, n, k):
     """nv_gemm_rows against the float64 product (the bound of nv_gemm's test); a
     second launch and a graph replay give the same bits."""
