@@ -364,18 +364,23 @@ __device__ __forceinline__ void score_queue(const uint32_t* queue, int count, in
     for (int j = lane; j < count; j += 2 * kWave) {
         const uint32_t e0 = queue[j];
         const uint32_t e1 = queue[j + kWave < count ? j + kWave : j];
-        const int ta = 8 * (int(e0 >> 9 & 31u) * stride + base + int(e0 >> 3 & 63u)) + int(e0 & 7u);
-        const int tb = 8 * (int(e1 >> 9 & 31u) * stride + base + int(e1 >> 3 & 63u)) + int(e1 & 7u);
+        // Chunk k * stride + base + lane (k < 32 and stride, base below 2^24:
+        // a full-rate 24-bit multiply).
+        const int ta = 8 * int(__umul24(e0 >> 9 & 31u, uint32_t(stride)) + uint32_t(base) + (e0 >> 3 & 63u)) +
+                       int(e0 & 7u);
+        const int tb = 8 * int(__umul24(e1 >> 9 & 31u, uint32_t(stride)) + uint32_t(base) + (e1 >> 3 & 63u)) +
+                       int(e1 & 7u);
         const float xa = __uint_as_float(e0 & 0xffff0000u), xb = __uint_as_float(e1 & 0xffff0000u);
-        // Floors first, both hashes interleaved, one rare branch each.
+        // Floors and both hashes before one rare branch, so the two hash
+        // chains interleave; a token below its floor scores below s0 and is
+        // skipped (its score would not change `best`).
         const uint32_t fa = TAB ? xfloors[int(e0 >> 16) - lxb] : hash_floor(p, xa);
         const uint32_t fb = TAB ? xfloors[int(e1 >> 16) - lxb] : hash_floor(p, xb);
         const uint32_t ma = hash_m(p.seed, uint32_t(ta)), mb = hash_m(p.seed, uint32_t(tb));
-        float sa = __builtin_nanf(""), sb = __builtin_nanf("");
-        if (ma >= fa) sa = score_from_m(xa, p.temperature, ma);
-        if (mb >= fb) sb = score_from_m(xb, p.temperature, mb);
-        consider(best, sa, ta);
-        consider(best, sb, tb);
+        if ((ma >= fa) | (mb >= fb)) {
+            if (ma >= fa) consider(best, score_from_m(xa, p.temperature, ma), ta);
+            if (mb >= fb) consider(best, score_from_m(xb, p.temperature, mb), tb);
+        }
     }
 }
 
