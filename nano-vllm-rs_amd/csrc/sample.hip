@@ -12,7 +12,9 @@
 // ln is nvr_logf, a fixed-bits logarithm shared with the host oracle, so CPU
 // and GPU agree on every Gumbel index.
 //
-// Layout of nv_sample_parallel (16-byte aligned rows, vocab % 8 == 0):
+// Layout of nv_sample_parallel (16-byte aligned rows, vocab % 8 == 0) from
+// 17 rows (up to 16: sample_partitions_full scores every token of 2048-token
+// partitions, then stage 3):
 //   1. sample_partitions_vec: one 256-thread block per (row, partition of
 //      2048 * kChunksPerLane tokens); every lane loads its chunks of 8 logits
 //      up front; the block stores the partition's greedy maximum (greedy rows)
@@ -41,6 +43,12 @@ constexpr int kRefPartition = 2048;
 // 2048 * kChunksPerLane tokens). Measured on MI355X at 256 x 151936: 2 is the
 // best for Gumbel and mixed batches (4 favours all-greedy batches by ~7%).
 constexpr int kChunksPerLane = 2;
+// Batches of at most this many rows score every token exactly in one pass
+// (sample_partitions_full) instead of pruning in a second one. Measured on
+// MI355X at 151936 tokens, half greedy / half T = 0.6 and all T = 0.6: 8 rows
+// 7.8 / 8.5 us against 10.7 / 11.1 us, 16 rows 9.7 / 11.0 against
+// 11.6 / 12.4 us; at 32 rows the two paths are even.
+constexpr int kFullScoreRows = 16;
 
 struct Best {
     float score;
@@ -170,6 +178,49 @@ __global__ __launch_bounds__(256) void sample_partitions_vec(const uint16_t* __r
         if (temperature > 0.0f && b.index != nvr::kNoIndex)
             score = nvr::gumbel_score(b.score, temperature, seeds[r], uint32_t(b.index));
         partial_scores[blockIdx.x] = score;
+        partial_ids[blockIdx.x] = b.index;
+    }
+}
+
+// Small batches: one pass in which Gumbel rows score every token of the
+// partition exactly (the greedy rows as sample_partitions_vec), then
+// sample_combine. At a few rows the batch's whole scoring is a few million
+// hashes and logarithms spread over every CU, cheaper than the pruning pass
+// and its extra dependent launch.
+template <int C>
+__global__ __launch_bounds__(256) void sample_partitions_full(const uint16_t* __restrict__ logits,
+                                                              const float* __restrict__ temps,
+                                                              const uint64_t* __restrict__ seeds,
+                                                              float* __restrict__ partial_scores,
+                                                              int* __restrict__ partial_ids, int vocab, int parts) {
+    constexpr int W = 2048 * C;
+    const int r = blockIdx.x / parts;
+    const int p = blockIdx.x - r * parts;
+    const int begin = p * W;
+    const int end = int(min(int64_t(begin) + W, int64_t(vocab)));
+    const uint16_t* row = logits + int64_t(r) * vocab;
+    uint4 w[C];
+    int t0[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        t0[c] = begin + 8 * int(threadIdx.x) + 2048 * c;
+        if (t0[c] < end) w[c] = nvr::load_stream(row + t0[c]);
+    }
+    const float temperature = temps[r];
+    const uint64_t seed = seeds[r];
+    Best b{-__builtin_inff(), nvr::kNoIndex};
+    if (temperature > 0.0f) {
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            if (t0[c] < end) scan_chunk<true>(b, w[c], t0[c], temperature, seed);
+    } else {
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            if (t0[c] < end) scan_chunk<false>(b, w[c], t0[c], 0.0f, 0);
+    }
+    b = block_argmax(b);
+    if (threadIdx.x == 0) {
+        partial_scores[blockIdx.x] = b.score;
         partial_ids[blockIdx.x] = b.index;
     }
 }
@@ -696,7 +747,11 @@ int launch_parallel(nv_context* c, const void* logits, const void* temps, const 
         return launch_resident<kResThreads>(c, l16, t, s, static_cast<int*>(out), ps, pi, batch, vocab,
                                             int((lane_chunks + 3) / 4 * 4));
     int parts;
-    if (vector_rows(logits, vocab)) {
+    if (vector_rows(logits, vocab) && batch <= kFullScoreRows) {
+        parts = int(ref_parts);  // 2048-token partitions: the most blocks the scratch allows
+        hipLaunchKernelGGL(sample_partitions_full<1>, dim3(unsigned(batch * parts)), dim3(256), 0, c->stream, l16, t, s,
+                           ps, pi, vocab, parts);
+    } else if (vector_rows(logits, vocab)) {
         // Never more partitions than the scratch holds (ceil(vocab / 2048)).
         parts = int((int64_t(vocab) + 2048 * kChunksPerLane - 1) / (2048 * kChunksPerLane));
         const int items = batch * parts;
