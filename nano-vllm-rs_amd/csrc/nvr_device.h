@@ -86,17 +86,12 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
 // -------------------------------------------------------- cross-lane ops ----
-// Butterfly exchange with lane ^ mask inside a wave64. For an IEEE sum the
-// butterfly leaves every lane with the same bits as the down-shift tree's
-// lane 0, because each level adds the same two operands (a+b == b+a).
-__device__ __forceinline__ float xor_lane(float v, int mask) { return __shfl_xor(v, mask, kWave); }
-__device__ __forceinline__ int xor_lane(int v, int mask) { return __shfl_xor(v, mask, kWave); }
-
 // DPP lane permutations (data-parallel primitives: the operand is read from
 // another lane of the same 16-lane row, no LDS traffic, and the compiler folds
 // the move into the consuming VALU op when it can).
 constexpr int kDppQuadXor1 = 0xB1;       // quad_perm [1,0,3,2]: lane ^ 1
 constexpr int kDppQuadXor2 = 0x4E;       // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppQuadReverse = 0x1B;    // quad_perm [3,2,1,0]: lane ^ 3
 constexpr int kDppRowRor8 = 0x128;       // row_ror:8 : lane ^ 8 inside a 16-lane row
 constexpr int kDppRowHalfMirror = 0x141; // row_half_mirror: lane i <-> 7-i inside each 8 lanes
 template <int CTRL>
@@ -112,6 +107,27 @@ __device__ __forceinline__ uint32_t dpp(uint32_t v) {
 __device__ __forceinline__ float swizzle_xor16(float v) {
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
 }
+
+// Butterfly exchange with lane ^ mask inside a wave64 (every lane active).
+// For an IEEE sum the butterfly leaves every lane with the same bits as the
+// down-shift tree's lane 0, because each level adds the same two operands
+// (a+b == b+a). Masks 1, 2 and 8 are one DPP move, 4 two (the 8-lane mirror
+// i <-> 7-i, then the quad reversal j <-> j ^ 3: i ^ 4 in all), 16 a swizzle
+// inside each 32-lane half; only 32 goes through the LDS crossbar.
+__device__ __forceinline__ uint32_t xor_lane_bits(uint32_t v, int mask) {
+    switch (mask) {
+        case 1: return dpp<kDppQuadXor1>(v);
+        case 2: return dpp<kDppQuadXor2>(v);
+        case 4: return dpp<kDppQuadReverse>(dpp<kDppRowHalfMirror>(v));
+        case 8: return dpp<kDppRowRor8>(v);
+        case 16: return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), 0x401F));
+        default: return uint32_t(__shfl_xor(int(v), mask, kWave));
+    }
+}
+__device__ __forceinline__ float xor_lane(float v, int mask) {
+    return __uint_as_float(xor_lane_bits(__float_as_uint(v), mask));
+}
+__device__ __forceinline__ int xor_lane(int v, int mask) { return int(xor_lane_bits(uint32_t(v), mask)); }
 
 // ------------------------------------------------------------- 1 / sqrt ----
 // Correctly rounded sqrt followed by a correctly rounded division: fixed bits
