@@ -438,6 +438,21 @@ def _edge_rows(batch, vocab, seed):
     return logits, temps, seeds
 
 
+@pytest.mark.parametrize("start,batch,vocab", [(0, 16, 40000), (3, 16, 40000), (0, 19, 12296), (0, 40, 40000),
+                                                (0, 100, 151936)])
+def test_sampling_partition_paths_on_edge_rows(gpu, start, batch, vocab):
+    """Below one row per CU: up to 16 rows every token is scored in one
+    partition pass; from 17 rows the partitions prune against the row's best
+    partial in a second pass. Both on the rows that stress pruning, special
+    values and temperatures (rows start .. start + batch of the edge rows),
+    against the oracle and the serial scan."""
+    logits, temps, seeds = _edge_rows(max(19, start + batch), vocab, 190 + batch)
+    logits, temps, seeds = (a[start:start + batch].copy() for a in (logits, temps, seeds))
+    want = ora.sample(logits, temps, seeds, batch, vocab, threads=8)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab), want)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab, parallel=False), want)
+
+
 @pytest.mark.parametrize("vocab", [3 * 4096 + 8, 40000, 90000, 131072, 163840, 163848])
 def test_sampling_large_batches(gpu, vocab):
     """From one row per CU, rows of up to 163840 tokens are sampled by one
