@@ -736,6 +736,8 @@ def test_gemm_few_rows_graph_replays(gpu):
     (32, 4096, 1024, True),   # two row tiles
     (17, 512, 2048, True),    # ragged second tile, k 2048
     (5, 16, 512, False),      # one column tile, k 512
+    (16, 4096, 1024, True),   # 8-wave blocks: all 16 rows in one norm pass
+    (12, 6144, 2048, True),   # 4-wave blocks: two norm passes, the second ragged
 ])
 def test_rms_gemm_norm_bits_and_gemm_bound(gpu, m, n, k, add):
     """nv_rms_gemm: the normalised rows and the updated residual equal the oracle's
@@ -778,7 +780,7 @@ def test_rms_gemm_rejects_unsupported_shapes(gpu):
 
 
 @pytest.mark.parametrize("m,inter,k,add", [(8, 3072, 1024, True), (1, 3072, 1024, False), (20, 512, 2048, True),
-                                           (5, 64, 512, False)])
+                                           (5, 64, 512, False), (16, 3072, 1024, True), (16, 2048, 1024, True)])
 def test_rms_gemm_silu_epilogue(gpu, m, inter, k, add):
     """nv_rms_gemm_silu: the norm outputs are the oracle's bits; gate_up (written in
     [gate | up] order from the tile-ordered weight) equals nv_rms_gemm's output with
