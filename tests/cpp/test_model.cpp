@@ -503,18 +503,18 @@ struct OracleShadow {
     }
 };
 
-TEST(forward_matches_the_oracle_stage_by_stage, "gpu") {
-    // Qwen3-0.6B widths (hidden 1024, intermediate 3072, 16/8 heads of 128,
-    // vocabulary 151936) with three layers, run eagerly so that every stage
-    // is observed: a prefill of 8 sequences x 128 tokens (1024 rows) sampling
-    // every sequence, then a decode step of those 8 sequences.
+// Qwen3-0.6B widths (hidden 1024, intermediate 3072, 16/8 heads of 128,
+// vocabulary 151936) with three layers, run eagerly so that every stage is
+// observed: a prefill of S sequences x P tokens sampling every sequence, then
+// a decode step of those S sequences.
+void stage_by_stage(std::size_t S, std::size_t P) {
     nvr::ModelConfig c;
     c.num_hidden_layers = 3;
     nvr::ModelOptions o;
     o.block_size = 256;
-    o.num_blocks = 16;
-    o.max_batch_tokens = 1024;
-    o.max_sequences = 8;
+    o.num_blocks = 2 * S;
+    o.max_batch_tokens = S * P;
+    o.max_sequences = S;
     o.max_model_len = 512;
     o.graphs = false;
     nvr::QwenModel model(c, o, random_weights(11, 0.03));
@@ -523,7 +523,6 @@ TEST(forward_matches_the_oracle_stage_by_stage, "gpu") {
     Tables t;
     t.block_size = 256;
     t.stride = 2;
-    const std::size_t S = 8, P = 128;
     std::vector<std::vector<int32_t>> prompts(S);
     std::vector<int32_t> starts(S, 0);
     std::vector<std::size_t> seqs(S);
@@ -568,6 +567,12 @@ TEST(forward_matches_the_oracle_stage_by_stage, "gpu") {
     std::printf("[decode: %zu stages] ", shadow.stages);
     CHECK(shadow.stages == 1 + 3 * 8 + 3);  // fused attention: no QkvRope stage
 }
+
+TEST(forward_matches_the_oracle_stage_by_stage, "gpu") { stage_by_stage(8, 128); }
+
+// 16 decode rows: the widest fused-norm step (one norm pass in 8-wave blocks
+// for qkv, two in 4-wave blocks for gate_up, the 16-row narrow GEMMs).
+TEST(forward_matches_the_oracle_stage_by_stage_16_rows, "gpu") { stage_by_stage(16, 64); }
 
 // ------------------------------------------------------ runner behaviour ---
 bool same_bits(const std::vector<std::vector<float>>& a, const std::vector<std::vector<float>>& b) {
