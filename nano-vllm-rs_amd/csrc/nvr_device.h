@@ -103,11 +103,6 @@ __device__ __forceinline__ uint32_t dpp(uint32_t v) {
     return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), CTRL, 0xF, 0xF, false));
 }
 
-// lane ^ 16 inside each 32-lane half (ds_swizzle bitmask mode: and 0x1f, xor 0x10).
-__device__ __forceinline__ float swizzle_xor16(float v) {
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
-}
-
 // Butterfly exchange with lane ^ mask inside a wave64 (every lane active).
 // For an IEEE sum the butterfly leaves every lane with the same bits as the
 // down-shift tree's lane 0, because each level adds the same two operands
@@ -120,7 +115,7 @@ __device__ __forceinline__ uint32_t xor_lane_bits(uint32_t v, int mask) {
         case 2: return dpp<kDppQuadXor2>(v);
         case 4: return dpp<kDppQuadReverse>(dpp<kDppRowHalfMirror>(v));
         case 8: return dpp<kDppRowRor8>(v);
-        case 16: return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), 0x401F));
+        case 16: return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), 0x401F));  // bitmask mode: and 0x1f, xor 0x10
         default: return uint32_t(__shfl_xor(int(v), mask, kWave));
     }
 }
