@@ -467,6 +467,27 @@ def test_sampling_large_batches(gpu, vocab):
     assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab, parallel=False), want)
 
 
+@pytest.mark.parametrize("greedy_rows", [1, 64, 128, 200, 255])
+def test_sampling_mixed_batches_one_row_per_cu(gpu, greedy_rows):
+    """One row per CU (the row-resident path), greedy rows spread over the
+    batch among Gumbel rows that include the pruning edge rows (flat rows,
+    extreme and subnormal temperatures, NaN and infinite logits), three calls
+    in a row on the same buffers, each against the oracle."""
+    batch, vocab = gpu.sm_count(), 151936
+    logits, temps, seeds = _edge_rows(batch, vocab, 400 + greedy_rows)
+    rng = np.random.default_rng(401 + greedy_rows)
+    temps = np.where(temps > 0, temps, np.float32(0.6)).astype(np.float32)  # NaN / <= 0 -> Gumbel
+    temps[rng.choice(batch, size=min(greedy_rows, batch - 1), replace=False)] = 0.0
+    want = ora.sample(logits, temps, seeds, batch, vocab, threads=8)
+    lb, tb, sb = up(gpu, logits), up(gpu, temps), up(gpu, seeds)
+    parts = -(-vocab // 2048)
+    ps, pi = gpu.alloc(batch * parts * 4), gpu.alloc(batch * parts * 4)
+    for _ in range(3):
+        out = gpu.alloc(batch * 4)
+        gpu.sample_parallel(lb, tb, sb, out, ps, pi, batch, vocab)
+        assert_bits_equal(out.download(np.int32, batch), want)
+
+
 def test_sampling_reference_golden_vectors(gpu):
     """All 20 last-position logit rows of the reference's validation run and
     the tokens its GPU greedy sampler picked (row 4: an exact tie, lower index
