@@ -51,6 +51,19 @@ def test_library_exports_every_declared_symbol():
     assert lib.nv_last_error() is not None
 
 
+def test_rust_build_snippet_compiles_every_source():
+    """The build.rs that INTEGRATION.md gives the Rust host lists its .hip
+    files by name; it must name exactly the library's sources, or a symbol
+    the header declares would be missing from a Rust build."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    listed = re.search(r"let sources = \[([^\]]*)\]", text)
+    assert listed, "INTEGRATION.md has no build.rs source list"
+    names = set(re.findall(r'"([a-z_]+)"', listed.group(1)))
+    csrc = os.path.join(ROOT, "nano-vllm-rs_amd", "csrc")
+    sources = {f[:-4] for f in os.listdir(csrc) if f.endswith(".hip")}
+    assert names == sources
+
+
 def test_host_seed_function_matches_oracle():
     for args in [(0, 0, 0), (0, 5, 3), (1234, 17, 100), (2**64 - 1, 1, 2)]:
         assert nvr.sampling_seed(*args) == ora.sampling_seed(*args)
