@@ -35,11 +35,15 @@
 //      adds); the last three run inside the lane. Three steps of K loads stay
 //      in flight behind the one being scored. Scores go to LDS.
 //   2. Block max, exp in place, the block sum in the reference's order.
-//   3. Values: 16 KB V tiles alternate between two LDS slots, one block
-//      barrier per tile; two more tiles are in flight in registers. Thread
-//      (g, d) runs its fma chain over the tile's tokens in order. Tokens of an
-//      invalid block are staged as -0.0 with p = +0, which leaves every chain
-//      value (including -0) unchanged, exactly as skipping them does.
+//   3. Values: 16 KB V tiles in LDS, one block barrier per tile. Thread
+//      (g, d) runs its fma chain over the tile's tokens in order. Launches of
+//      at most one block per CU whose tiles lie in whole blocks (kStreamed)
+//      stream each tile from memory straight into one of four LDS slots
+//      (global_load_lds), three tiles ahead, and skip a tile of an invalid
+//      block. Otherwise tiles alternate between two LDS slots with two more
+//      in flight in registers; tokens of an invalid block are staged as -0.0
+//      with p = +0, which leaves every chain value (including -0) unchanged,
+//      exactly as skipping them does.
 // Other head dims, unaligned operands and caches of more than 2^31 token rows
 // use a direct kernel with the same arithmetic.
 #include "../../include/nano_hip.h"
@@ -73,6 +77,17 @@ __device__ __forceinline__ float fold8(const float* w) {
     return ((w[0] + w[4]) + (w[2] + w[6])) + ((w[1] + w[5]) + (w[3] + w[7]));
 }
 
+// Block barrier once this wave's vector memory operations have dropped to N
+// outstanding and its LDS operations to none.
+template <int N>
+__device__ __forceinline__ void stream_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Block barrier over LDS only: unlike __syncthreads it does not wait for
+// outstanding vector memory operations (the streamed V tiles).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Physical token index of a table entry and logical token, or -1.
 __device__ __forceinline__ int64_t phys_token(int entry, int t, int bs, int blocks) {
     return entry >= 0 && entry < blocks ? int64_t(entry) * bs + t % bs : int64_t(-1);
@@ -96,13 +111,17 @@ struct OrderedLayout {
     static constexpr int kKStage = kWaves * kQuads * kKRow;
     static constexpr int kVStage = 2 * kVTile * DIM * 2;
     static constexpr int kStageBytes = kKStage > kVStage ? kKStage : kVStage;
+    static constexpr int kSlots = 4;  // kStreamed's V slots (they reuse the K rows' LDS)
+    static constexpr int kSlotBytes = kVTile * DIM * 2;
+    static constexpr int kStreamStage = kKStage > kSlots * kSlotBytes ? kKStage : kSlots * kSlotBytes;
     static_assert(kKLoads * kRowsPerLoad == kQuads && kVLoads * kThreads == kVTile * kPieces, "tiles");
 };
 
 // How a logical token finds its physical row: kAnyBs divides by the block
 // size; kPow2 shifts (bs a power of two); kAligned (bs a power of two holding
 // whole K steps and V tiles) looks the block entry up once per step or tile.
-constexpr int kAnyBs = 0, kPow2 = 1, kAligned = 2;
+// kStreamed is kAligned with the V tiles streamed into LDS slots.
+constexpr int kAnyBs = 0, kPow2 = 1, kAligned = 2, kStreamed = 3;
 
 // The q/k norm + RoPE + KV-slot write that FUSED blocks run first (the
 // decode-batch entry point); unused otherwise.
@@ -130,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     extern __shared__ __align__(16) unsigned char smem[];
     float* probs = reinterpret_cast<float*>(smem);                          // [HPB][score_stride]
     unsigned char* stage = smem + sizeof(float) * HPB * score_stride;       // K rows (phase 1) / V slots (phase 3)
-    int* ltable = reinterpret_cast<int*>(stage + L::kStageBytes);           // the row's block-table entries
+    int* ltable = reinterpret_cast<int*>(stage + L::kStageBytes);           // the row's block-table entries (kAnyBs, kPow2)
     __shared__ float red_max[HPB][kWaves];
     __shared__ float red_sum[HPB][2 * kWaves];
 
@@ -204,7 +223,7 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     const int* table = tables + int64_t(seq) * stride;
     const int nent = (ctx - 1) / bs + 1;
     int lane_entry = -1;
-    if constexpr (TABLE == kAligned) {
+    if constexpr (TABLE >= kAligned) {
         if (lane < nent) lane_entry = table[lane];
     } else {
         for (int i = threadIdx.x; i < nent; i += kThreads) ltable[i] = table[i];
@@ -267,7 +286,7 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     // kAligned: lane offsets of a step's rows from the step's first row.
     const int klane = (wave * kQuads + lrow) * int(token_stride);
     auto issue = [&](uint4 (&kb)[kKLoads], int s) {
-        if constexpr (TABLE == kAligned) {
+        if constexpr (TABLE >= kAligned) {
             const uint16_t* base = group_base(kcol, group_entry(s * kStep), s * kStep);
 #pragma unroll
             for (int k = 0; k < kKLoads; ++k)
@@ -296,7 +315,7 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
             nvr::unpack8(*reinterpret_cast<const uint4*>(krows + tq * kKRow + 16 * (4 * j + a)), kf[j]);
         const int t = s * kStep + wave * kQuads + tq;
         const bool live = t < ctx;
-        const bool valid = live && (TABLE == kAligned ? entry_ok(group_entry(s * kStep))
+        const bool valid = live && (TABLE >= kAligned ? entry_ok(group_entry(s * kStep))
                                                       : phys(min(t, ctx - 1)) >= 0);
 #pragma unroll
         for (int g = 0; g < HPB; ++g) {
@@ -358,7 +377,7 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     // leaves every chain value unchanged, exactly as skipping them does.
     const uint16_t* vcol = vc + int64_t(kvhead) * DIM;
     auto load_vtile = [&](uint4 (&r)[kVLoads], bool (&ok)[kVLoads], int t0) {
-        if constexpr (TABLE == kAligned) {
+        if constexpr (TABLE >= kAligned) {
             const int e = group_entry(t0);
             const uint16_t* base = group_base(vcol, e, t0);
 #pragma unroll
@@ -380,9 +399,46 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     };
     bool okW[kVLoads], okX[kVLoads], okY[kVLoads];
     uint4 rW[kVLoads], rX[kVLoads], rY[kVLoads];
-    load_vtile(rW, okW, 0);
-    load_vtile(rX, okX, kVTile);
-    load_vtile(rY, okY, 2 * kVTile);
+    if constexpr (TABLE != kStreamed) {
+        load_vtile(rW, okW, 0);
+        load_vtile(rX, okX, kVTile);
+        load_vtile(rY, okY, 2 * kVTile);
+    }
+    // kStreamed: a tile goes from memory straight into its LDS slot. Load u
+    // of wave w brings kRowsPerLoad whole token rows (1 KB): tokens
+    // (4w + u) * kRowsPerLoad onwards, lane l landing at byte 16 l. The loads
+    // are inline asm, so the compiler (which would make every later LDS read
+    // wait for all of them) never sees them: stream_wait orders them. M0
+    // holds the LDS address and is restored after each load. Every address
+    // lies in an allocated block (group_base), and a tile is only issued when
+    // it starts inside the context.
+    const int ntiles = (ctx + kVTile - 1) / kVTile;
+    using LdsBytes = __attribute__((address_space(3))) unsigned char*;
+    const uint32_t stage_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsBytes)stage));
+    auto stream_vtile = [&](int t0, int slot) {
+        const uint16_t* base = group_base(vcol, group_entry(t0), t0);
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(stage_lds + slot * L::kSlotBytes + wave * 4096);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint16_t* src = base + ((wave * 4 + u) * kRowsPerLoad + lrow) * int(token_stride) + 8 * lpiece;
+            uint32_t saved;
+            asm volatile(
+                "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+                "s_mov_b32 m0, %0"
+                : "=&s"(saved)
+                : "v"(src), "s"(dst + u * 1024)
+                : "memory");
+        }
+    };
+    static_assert(TABLE != kStreamed || 4 * kWaves * 1024 == L::kSlotBytes, "a tile is four 1 KB loads per wave");
+    // Block barrier once every wave's loads of the tile to be consumed have
+    // landed, `ahead` tiles (four loads each) having been issued after it.
+    auto stream_wait = [&](int ahead) {
+        static_assert(L::kSlots == 4, "up to two tiles ahead");
+        if (ahead >= 2) stream_barrier<8>();
+        else if (ahead == 1) stream_barrier<4>();
+        else stream_barrier<0>();
+    };
 
     // ---- 2. max, exp, block sum ----
 #pragma unroll
@@ -391,6 +447,9 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
         if (lane == 0) red_max[g][wave] = m[g];
     }
     __syncthreads();
+    if constexpr (TABLE == kStreamed) {  // every wave is past its scores: the K rows' LDS is free
+        for (int i = 0; i < L::kSlots - 1 && i < ntiles; ++i) stream_vtile(i * kVTile, i);
+    }
     float den[HPB];
 #pragma unroll
     for (int g = 0; g < HPB; ++g) {
@@ -405,7 +464,10 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
         sum = half_wave_sum(sum);
         if ((lane & 31) == 0) red_sum[g][2 * wave + (lane >> 5)] = sum;
     }
-    __syncthreads();
+    if constexpr (TABLE == kStreamed)
+        lds_barrier();  // leaves the V tiles in flight
+    else
+        __syncthreads();
 #pragma unroll
     for (int g = 0; g < HPB; ++g) den[g] = fold8(red_sum[g]);
 
@@ -478,6 +540,17 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
         for (; j + 8 <= n; j += 8) eight(j);
         for (; j < n; ++j) acc = __builtin_fmaf(pg[t0 + j], nvr::bf16_to_f32(vt[j * DIM]), acc);
     };
+    if constexpr (TABLE == kStreamed) {
+        // Tile i is consumed while tiles i + 1 and i + 2 stream in; the
+        // barrier before each issue also frees the slot it refills.
+        for (int i = 0; i < ntiles; ++i) {
+            stream_wait(min(ntiles - 1 - i, L::kSlots - 2));
+            const int next = i + L::kSlots - 1;
+            if (next < ntiles) stream_vtile(next * kVTile, next % L::kSlots);
+            const int t0 = i * kVTile;
+            if (entry_ok(group_entry(t0))) consume(i % L::kSlots, t0);  // an invalid block adds no V term
+        }
+    } else
     // Three register tiles in fixed roles keep two tiles in flight while one
     // is consumed. The loads past the context stay unconditional (they hit
     // token 0 of block 0 in L2; a branch would drain the load queue).
@@ -582,8 +655,22 @@ void launch_layout(nv_context* c, const uint16_t* q, uint16_t* k, uint16_t* v, c
     const int shift = pow2 ? __builtin_ctz(unsigned(bs)) : 0;
     // kAligned also needs the row's table in one wave (at most 64 entries) and
     // in-block offsets that fit in int32.
-    if (pow2 && bs >= L::kStep && bs >= L::kVTile && (max_context - 1) / bs < kWave &&
-        int64_t(bs) * kvh * DIM < (int64_t(1) << 31))
+    const bool aligned = pow2 && bs >= L::kStep && bs >= L::kVTile && (max_context - 1) / bs < kWave &&
+                         int64_t(bs) * kvh * DIM < (int64_t(1) << 31);
+    // kStreamed's four V slots take the LDS a second block per CU would use:
+    // it runs when the launch has at most one block per CU anyway (decode
+    // batches up to 32 rows at Qwen3 shapes). Measured on MI355X at 8 rows x
+    // 1024 tokens: 27.7 -> 23.7 us; 8-row serving step 1.075 -> 1.035 ms.
+    if constexpr (!OCC) {
+        const int64_t cus = c->cu_count > 0 ? c->cu_count : 256;
+        if (aligned && int64_t(rows) * (qh / HPB) <= cus) {
+            hipLaunchKernelGGL((attention_ordered<DIM, HPB, kStreamed, false, FUSED>), grid, dim3(kThreads),
+                               sizeof(float) * HPB * score_stride + L::kStreamStage, c->stream, q, k, v, p, s, t, o,
+                               qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride, fa);
+            return;
+        }
+    }
+    if (aligned)
         hipLaunchKernelGGL((attention_ordered<DIM, HPB, kAligned, OCC, FUSED>), grid, dim3(kThreads), lds, c->stream,
                            q, k, v, p, s, t, o, qh, kvh, bs, shift, blocks, stride, batch, max_context, score_stride,
                            fa);

@@ -604,6 +604,24 @@ def test_attention_aligned_blocks_with_holes_mid_context(gpu):
     _attention_case(gpu, 235, pos, seqs, 16, 8, 128, bs, batch, stride, 4096, holes=holes)
 
 
+@pytest.mark.parametrize("extra_rows", [0, 1])
+def test_attention_aligned_streamed_and_register_tiles(gpu, extra_rows):
+    """256-token blocks with a GQA pair per block at exactly one block per CU
+    (the V tiles stream from memory into LDS slots) and with one row more
+    (the V tiles pass through registers): contexts that end on, just past and
+    inside 64-token tiles, one-tile contexts, and invalid table entries in the
+    middle and at the end of contexts."""
+    qh, kvh, dim, bs, stride, max_context = 16, 8, 128, 256, 16, 4096
+    rows = gpu.sm_count() // (qh // 2) + extra_rows
+    rng = np.random.default_rng(240 + extra_rows)
+    pos = rng.integers(0, 2048, size=rows)
+    edges = [0, 62, 63, 64, 127, 128, 191, 192, 255, 256, 4095, 1000]
+    pos[:len(edges)] = edges
+    holes = [(1 * stride + 0, -1), (11 * stride + 2, rows * stride), (12 * stride + 3, -5), (13 * stride, -1)]
+    _attention_case(gpu, 245 + extra_rows, pos, np.arange(rows), qh, kvh, dim, bs, rows, stride, max_context,
+                    holes=holes)
+
+
 @pytest.mark.parametrize("rows,bs,seed", [(8, 256, 300), (32, 256, 310), (8, 16, 320), (5, 7, 330), (32, 16, 340),
                                          (32, 7, 350)])
 def test_attention_qkv_rope_matches_separate_launches(gpu, rows, bs, seed):
