@@ -319,6 +319,19 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     // 8a .. 8a+7, i.e. pieces 4j + a (j < P) of token tq.
     const int tq = lane >> 2, a = lane & 3;
     const int lrow = lane / kPieces, lpiece = lane % kPieces;
+    // kStreamed: this lane's byte offsets, from a V tile's first row, of its
+    // four 16-byte loads (phase 3). Computed here and made opaque so that they
+    // stay in registers of their own: computed after the scores, they would
+    // reuse the registers of the K loads still in flight past the last step,
+    // and the compiler would make the V loads wait for those.
+    uint32_t voff[4] = {};
+    if constexpr (TABLE == kStreamed) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            voff[u] = uint32_t((((wave * 4 + u) * kRowsPerLoad + lrow) * int(token_stride) + 8 * lpiece) * 2);
+            asm volatile("" : "+v"(voff[u]));
+        }
+    }
     unsigned char* krows = stage + wave * kQuads * kKRow;
     const uint16_t* kcol = kc + int64_t(kvhead) * DIM + 8 * lpiece;
     float qf[HPB][P][8];
@@ -472,17 +485,16 @@ __global__ __launch_bounds__(kThreads) void attention_ordered(
     const int ntiles = (ctx + kVTile - 1) / kVTile;
     const uint32_t stage_lds = lds_address(stage);
     auto stream_vtile = [&](int t0, int slot) {
-        const uint16_t* base = group_base(vcol, group_entry(t0), t0);
+        const uint16_t* base = group_base(vcol, group_entry(t0), t0);  // uniform: scalar base
         const uint32_t dst = __builtin_amdgcn_readfirstlane(stage_lds + slot * L::kSlotBytes + wave * 4096);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const uint16_t* src = base + ((wave * 4 + u) * kRowsPerLoad + lrow) * int(token_stride) + 8 * lpiece;
             uint32_t saved;
             asm volatile(
-                "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+                "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
                 "s_mov_b32 m0, %0"
                 : "=&s"(saved)
-                : "v"(src), "s"(dst + u * 1024)
+                : "v"(voff[u]), "s"(base), "s"(dst + u * 1024)
                 : "memory");
         }
     };
