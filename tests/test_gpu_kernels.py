@@ -604,6 +604,34 @@ def test_attention_aligned_blocks_with_holes_mid_context(gpu):
     _attention_case(gpu, 235, pos, seqs, 16, 8, 128, bs, batch, stride, 4096, holes=holes)
 
 
+@pytest.mark.parametrize("rows", [8, 32])
+def test_attention_streamed_tiles_signed_zero_and_tiny_values(gpu, rows):
+    """The streamed-tile value chain (one block per CU, head dim 128, 256-token
+    blocks; one q head per block at 8 rows, a GQA pair at 32): scores spread
+    so that many probabilities are subnormal or zero (q_std 6), V dimensions
+    of the smallest subnormals, whose products and outputs round to -0 or +0
+    (the sign must survive the chain), and of tiny values with subnormal
+    outputs; contexts ending on, just past and inside 64-token tiles."""
+    qh, kvh, dim, bs, stride, max_context = 16, 8, 128, 256, 16, 4096
+    rng = np.random.default_rng(260 + rows)
+    blocks = rows * stride
+    tables = rng.permutation(blocks).astype(np.int32)
+    pos = rng.integers(0, 2048, size=rows).astype(np.int32)
+    pos[:8] = [1023, 63, 64, 127, 150, 4095, 0, 700]
+    seqs = np.arange(rows, dtype=np.int32)
+    q = ora.normal_bf16((rows, qh, dim), 261, 0.0, 6.0)
+    kc = ora.normal_bf16((blocks, bs, kvh, dim), 262, 0.0, 1.0)
+    vc = ora.normal_bf16((blocks, bs, kvh, dim), 263, 0.0, 1.0)
+    vc[..., 16:20] = 0x8001  # the smallest bf16 subnormals, negative and positive:
+    vc[..., 20:24] = 0x0001  # products and outputs round to signed zeros
+    vc[..., 24:32] = ora.normal_bf16((blocks, bs, kvh, 8), 264, 0.0, 1e-38)  # subnormal outputs
+    want = ora.attention(q, kc, vc, pos, seqs, tables, rows, qh, kvh, dim, bs, blocks, stride, rows, max_context,
+                         threads=8)
+    got = _attention(gpu, q, kc, vc, pos, seqs, tables, rows, qh, kvh, dim, bs, blocks, stride, rows, max_context)
+    assert_bits_equal(got, want)
+    assert (want == 0x8000).any() and (want == 0).any()  # both signed zeros occur
+
+
 @pytest.mark.parametrize("extra_rows", [0, 1])
 def test_attention_aligned_streamed_and_register_tiles(gpu, extra_rows):
     """256-token blocks with a GQA pair per block at exactly one block per CU
