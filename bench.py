@@ -85,6 +85,9 @@ class Hip:
         self.check(self.lib.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
         return e
 
+    def destroy(self, e):
+        self.check(self.lib.hipEventDestroy(e), "hipEventDestroy")
+
     def record(self, e, stream):
         self.check(self.lib.hipEventRecord(e, stream), "hipEventRecord")
 
@@ -233,18 +236,48 @@ def time_graph(gpu, hip, graph, reps, warmup):
     gpu.sync()
     hip.device_sync()
     a, b = hip.event(), hip.event()
-    hip.record(a, stream)
-    for _ in range(reps):
-        graph.replay()
-    hip.record(b, stream)
-    ms = hip.elapsed_ms(a, b)
+    try:
+        hip.record(a, stream)
+        for _ in range(reps):
+            graph.replay()
+        hip.record(b, stream)
+        ms = hip.elapsed_ms(a, b)
+    finally:
+        # Events hold runtime resources; a timing loop that never released
+        # them ended in a crash inside hipGraphLaunch after ~10^3 calls.
+        hip.destroy(a)
+        hip.destroy(b)
     gpu.sync()
     hip.device_sync()
     return ms / reps
 
 
 # ------------------------------------------------------ per-kernel loops ---
-def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=()):
+LAYOUT_SEEDS = (1, 2, 3, 4, 5)
+
+
+def add_spikes(buf, rows, vocab, count, amount, rng):
+    """Adds `amount` to one random logit in each of `count` random rows of a
+    bf16 [rows, vocab] device buffer (rounded once to bf16)."""
+    for r in rng.choice(rows, count, replace=False):
+        off = (int(r) * vocab + int(rng.integers(0, vocab))) * 2
+        cell = buf.slice(off, 2)
+        value = nvr.bf16_values(cell.download(np.uint16, 1))[0]
+        cell.upload(nvr.bf16_bits(np.array([value + amount], np.float32)))
+
+
+def slot_layouts(tokens, cache_blocks):
+    """Slot layouts of the sweep: identity slots, then the block permutations
+    of LAYOUT_SEEDS (slot = perm[t // 256] * 256 + t % 256)."""
+    t = np.arange(tokens)
+    out = [("@identity", t.astype(np.int32))]
+    for seed in LAYOUT_SEEDS:
+        perm = np.random.default_rng(seed).permutation(cache_blocks)
+        out.append((f"@perm{seed}", (perm[t // BS] * BS + t % BS).astype(np.int32)))
+    return out
+
+
+def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=(), sweep_layouts=True):
     """(name, workload, launch closures over rotating sets, bytes per launch, rows per launch) per case."""
     cases = []
 
@@ -292,7 +325,10 @@ def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=()):
         cases.append(("silu_8192x6144", "SiLU(gate)*up [8192,6144] -> [8192,3072]",
                       [lambda i=i, T=T: gpu.silu_mul(gus[i], acts[i], T, I) for i in range(s)], bytes_silu(T, I), T))
 
-    # q/k norm + RoPE + KV write at 2048 and 8192 tokens, uniform random positions.
+    # q/k norm + RoPE + KV write at 2048, 4096 and 8192 tokens, uniform random
+    # positions; slots from a random permutation of the cache blocks. At 8192
+    # tokens the same buffers are also written through identity slots and five
+    # more block permutations (cases "qkv_rope_8192@<layout>").
     for T in (2048, 4096, 8192):
         if not want(f"qkv_rope_{T}"):
             continue
@@ -301,7 +337,7 @@ def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=()):
         blocks = T // BS
         perm = rng.permutation(blocks)
         slots = (perm[np.arange(T) // BS] * BS + np.arange(T) % BS).astype(np.int32)
-        pb, sb = fill.ints(pos), fill.ints(slots)
+        pb = fill.ints(pos)
         per = T * HEADS * D * 2 * 2
         s = sets_for(per)
         qkvs = [fill.normal(T * HEADS * D * 2) for _ in range(s)]
@@ -310,11 +346,14 @@ def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=()):
         vcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
         qn, kn = fill.normal(D * 2, 1.0, 0.02), fill.normal(D * 2, 1.0, 0.02)
         nbytes = bytes_qkv_rope(T, len(np.unique(pos)))
-        cases.append((f"qkv_rope_{T}", f"q/k RMSNorm + NeoX RoPE + KV write, {T} tokens",
-                      [lambda i=i, T=T, pb=pb, sb=sb, blocks=blocks, qkvs=qkvs, qos=qos, kcs=kcs, vcs=vcs, qn=qn,
-                       kn=kn: gpu.qkv_rope_cached(qkvs[i], qn, kn, pb, sb, qos[i], kcs[i], vcs[i], T, QH, KVH, D, BS,
-                                                  blocks, EPS, chain.rope, MAX_POS) for i in range(s)],
-                      nbytes, T))
+        layouts = [("", slots)] + (slot_layouts(T, blocks) if T == 8192 and sweep_layouts else [])
+        for tag, sl in layouts:
+            sb = fill.ints(sl)
+            cases.append((f"qkv_rope_{T}{tag}", f"q/k RMSNorm + NeoX RoPE + KV write, {T} tokens",
+                          [lambda i=i, T=T, pb=pb, sb=sb, blocks=blocks, qkvs=qkvs, qos=qos, kcs=kcs, vcs=vcs, qn=qn,
+                           kn=kn: gpu.qkv_rope_cached(qkvs[i], qn, kn, pb, sb, qos[i], kcs[i], vcs[i], T, QH, KVH, D,
+                                                      BS, blocks, EPS, chain.rope, MAX_POS) for i in range(s)],
+                          nbytes, T))
 
     # Embedding gather, 16384 tokens from a [151936, 1024] table (three tables).
     T = 16384
@@ -326,20 +365,30 @@ def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=()):
                       [lambda j=j, T=T: gpu.embedding(toks[j], tables[j % 3], eouts[j], T, H, V) for j in range(6)],
                       bytes_embedding(T, H), T))
 
-    # Paged KV write, k/v [16384, 8, 128] into per-layer caches.
+    # Paged KV write, k/v [16384, 8, 128] into the per-layer caches of a
+    # 28-layer layout ([128, 256, 8, 128] per layer and per K/V, 3.5 GiB in
+    # all); launch l writes layer l from source set l mod 5. Slots come from a
+    # random permutation of the 128 blocks (the first 64 are written); the
+    # same launches also run with identity slots and five more permutations
+    # (cases "kv_write_16384@<layout>").
     if want("kv_write_16384"):
-        blocks = T // BS
-        s = sets_for(4 * T * KVH * D * 2)
-        ks = [fill.normal(T * KVH * D * 2) for _ in range(s)]
-        vs = [fill.normal(T * KVH * D * 2) for _ in range(s)]
-        kcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
-        vcs = [gpu.alloc(blocks * BS * KVH * D * 2) for _ in range(s)]
-        perm = np.random.default_rng(7).permutation(blocks)
-        sl = fill.ints((perm[np.arange(T) // BS] * BS + np.arange(T) % BS).astype(np.int32))
-        cases.append(("kv_write_16384", "paged KV write k,v [16384,8,128]",
-                      [lambda i=i, T=T, blocks=blocks: gpu.kv_write(ks[i], vs[i], sl, kcs[i], vcs[i], T, KVH, D, BS,
-                                                                   blocks) for i in range(s)],
-                      bytes_kv_write(T), T))
+        cache_blocks = 128
+        nsrc = 5
+        ks = [fill.normal(T * KVH * D * 2) for _ in range(nsrc)]
+        vs = [fill.normal(T * KVH * D * 2) for _ in range(nsrc)]
+        kcs = [gpu.alloc(cache_blocks * BS * KVH * D * 2) for _ in range(LAYERS)]
+        vcs = [gpu.alloc(cache_blocks * BS * KVH * D * 2) for _ in range(LAYERS)]
+        perm = np.random.default_rng(7).permutation(cache_blocks)
+        layouts = [("", (perm[np.arange(T) // BS] * BS + np.arange(T) % BS).astype(np.int32))]
+        if sweep_layouts:
+            layouts += slot_layouts(T, cache_blocks)
+        for tag, slots in layouts:
+            sl = fill.ints(slots)
+            cases.append((f"kv_write_16384{tag}", "paged KV write k,v [16384,8,128] into a 28-layer cache "
+                          "[128,256,8,128] per layer",
+                          [lambda l=l, sl=sl: gpu.kv_write(ks[l % nsrc], vs[l % nsrc], sl, kcs[l], vcs[l], T, KVH, D,
+                                                           BS, cache_blocks) for l in range(LAYERS)],
+                          bytes_kv_write(T), T))
 
     # Paged attention, decode: 64 sequences at context 4096 (one query row each).
     if want("attention_decode_64x4096"):
@@ -411,13 +460,16 @@ def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=()):
                                                           chain.rope, MAX_POS) for i in range(fsets)],
                       fbytes, fb))
 
-    # Sampling 256 x 151936: rows 0-127 greedy, 128-255 Gumbel at T=0.6.
+    # Sampling 256 x 151936: logits ~N(0,3), 1% of the rows (3) with +20 added
+    # at one random token; rows 0-127 greedy, 128-255 Gumbel at T=0.6.
     if not want("sampling_256x151936", "sampling_greedy", "sampling_gumbel"):
         return cases
     B = 256
     per = B * V * 2
     s = sets_for(per)
     logits = [fill.normal(B * V * 2, 0.0, 3.0) for _ in range(s)]
+    for i, buf in enumerate(logits):
+        add_spikes(buf, B, V, round(0.01 * B), 20.0, np.random.default_rng(500 + i))
     parts = -(-V // 2048)
     ps, pi = gpu.alloc(B * parts * 4), gpu.alloc(B * parts * 4)
     out = gpu.alloc(B * 4)
@@ -675,22 +727,166 @@ def cpu_baseline(tokens: int, layers: int, runs: int = 5) -> dict:
 
 
 # ------------------------------------------------------------------ main ---
+def warm_up(gpu, hip, seconds, graph=None):
+    """Sustained load before anything is timed: the GPU's clocks settle over
+    the first ~0.1-1 s of work, and launches timed earlier run up to ~8% slow.
+    Replays `graph` (the step), or 512 MiB device copies when there is none
+    (few dispatches, for runs under a kernel tracer)."""
+    if seconds <= 0:
+        return
+    t0 = time.perf_counter()
+    if graph is None:
+        n = 512 << 20
+        a, b = gpu.alloc(n), gpu.alloc(n)
+        stream = gpu.stream()
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(8):
+                hip.copy_d2d(b.ptr, a.ptr, n, stream)
+            gpu.sync()
+        return
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            graph.replay()
+        gpu.sync()
+
+
+# ---------------------------------------------------- kernel-time child ----
+TRACE_NOTE = "rocprofv3 --kernel-trace of a child run of this script over the same kernel cases (median duration)"
+
+
+def trace_child(out_dir, rounds, only) -> int:
+    """Child mode (under rocprofv3 --kernel-trace): the kernel cases only, in
+    order, after a copy warm-up; writes the case list with its dispatch counts
+    to out_dir/cases.json so the parent can assign the trace's dispatches."""
+    hip = Hip()
+    gpu = nvr.Gpu(0)
+    fill = Filler(gpu, hip)
+    chain = Chain(gpu, fill, 8192, 1)
+    cases = kernel_cases(gpu, hip, fill, chain, only)
+    gpu.sync()
+    warm_up(gpu, hip, 1.0)
+    order = []
+    for name, _, launches, _, _ in cases:
+        run_kernel_case(gpu, hip, launches, rounds)
+        order.append({"case": name, "launches": len(launches), "warm": 2, "rounds": rounds})
+    gpu.sync()
+    with open(os.path.join(out_dir, "cases.json"), "w") as f:
+        json.dump(order, f)
+    return 0
+
+
+def assign_dispatches(order, disp) -> tuple[dict, str]:
+    """Splits the traced dispatches (start ns, duration us, kernel name), set-up
+    kernels removed, over the cases in the order the child ran them: each case
+    is (warm + rounds) x launches consecutive dispatches of one kernel, and its
+    figure is the median of the timed ones."""
+    import statistics
+
+    disp = sorted(disp)
+    result, i = {}, 0
+    for c in order:
+        n = (c["warm"] + c["rounds"]) * c["launches"]
+        group = disp[i:i + n]
+        i += n
+        names = {g[2] for g in group}
+        if len(group) != n or len(names) != 1:
+            return {}, f"kernel trace does not line up with the cases at {c['case']}"
+        timed = [g[1] for g in group[c["warm"] * c["launches"]:]]
+        short = next(iter(names)).replace("(anonymous namespace)::", "").replace("void ", "").split("(")[0]
+        result[c["case"]] = (short, statistics.median(timed), len(timed))
+    if i != len(disp):
+        return {}, f"kernel trace has {len(disp) - i} dispatches past the last case"
+    return result, "ok"
+
+
+def kernel_times(rounds, only, timeout_s=420) -> tuple[dict, str]:
+    """{case: (kernel name, median kernel us, timed dispatches)} from a child
+    run of this script under rocprofv3 --kernel-trace, and a status note.
+    Runs before this process touches the GPU; empty when rocprofv3 is absent
+    or the child fails (the line then carries event times only)."""
+    import csv
+    import glob
+    import shutil
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3" if os.path.exists("/opt/rocm/bin/rocprofv3")
+                                         else None)
+    if prof is None:
+        return {}, "rocprofv3 not found"
+    out = tempfile.mkdtemp(prefix="nvr_trace_")
+    try:
+        cmd = [prof, "--kernel-trace", "-f", "csv", "-d", out, "-o", "kt", "--", sys.executable,
+               os.path.abspath(__file__), "--trace-child", out, "--kernel-rounds", str(rounds)]
+        if only:
+            cmd += ["--only", ",".join(only)]
+        done = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s, cwd=out,
+                              env=dict(os.environ, TMPDIR=os.environ.get("TMPDIR", "/tmp")))
+        cases_path = os.path.join(out, "cases.json")
+        if not os.path.exists(cases_path):
+            return {}, f"kernel-trace child failed (status {done.returncode}): {done.stderr.strip()[-300:]}"
+        order = json.load(open(cases_path))
+        disp = []
+        for path in glob.glob(os.path.join(out, "**", "*kernel_trace.csv"), recursive=True):
+            with open(path, newline="") as f:
+                for rec in csv.DictReader(f):
+                    name = rec["Kernel_Name"]
+                    if name.startswith("__amd_rocclr") or "rope_table" in name:
+                        continue  # set-up copies and the RoPE table, before any case runs
+                    start, end = int(rec["Start_Timestamp"]), int(rec["End_Timestamp"])
+                    disp.append((start, (end - start) / 1e3, name))
+        return assign_dispatches(order, disp)
+    except subprocess.TimeoutExpired:
+        return {}, f"kernel-trace child exceeded {timeout_s} s"
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+
+
+def fold_layouts(kernels):
+    """Moves the slot-layout cases ("<case>@<layout>") under their case and
+    adds the min and median over all layouts (the case's own included)."""
+    for name in [k for k in kernels if "@" in k]:
+        base, tag = name.split("@", 1)
+        entry = kernels.pop(name)
+        if base in kernels:
+            kernels[base].setdefault("layouts", {})[tag] = {k: entry[k] for k in ("us", "frac", "kernel_us", "kernel_frac")
+                                                            if k in entry}
+    for base, entry in kernels.items():
+        if "layouts" not in entry:
+            continue
+        rows = [entry] + list(entry["layouts"].values())
+        summary = {"layouts": len(rows), "default": entry.get("slot_layout", "")}
+        for key in ("frac", "kernel_frac"):
+            vals = [r[key] for r in rows if key in r]
+            if len(vals) == len(rows):
+                summary[f"{key}_min"] = round(min(vals), 4)
+                summary[f"{key}_median"] = round(float(np.median(vals)), 4)
+        entry["layout_sweep"] = summary
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warm-seconds", type=float, default=1.5,
+                    help="sustained replays of the step before anything is timed (clocks settle)")
     ap.add_argument("--tokens", type=int, default=8192)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
     ap.add_argument("--no-decode", action="store_true", help="skip the forward runner's decode-step lines")
+    ap.add_argument("--no-kernel-trace", action="store_true",
+                    help="skip the child run under rocprofv3 that gives each case's kernel duration")
     ap.add_argument("--kernel-rounds", type=int, default=5)
     ap.add_argument("--only", default="", help="comma-separated kernel cases to run (implies --no-cpu, skips the step)")
+    ap.add_argument("--trace-child", metavar="DIR", help=argparse.SUPPRESS)
     ap.add_argument("--pmc-summary", nargs="+", metavar=("KIND", "DIR"),
                     help="print the table of rocprofv3 counter runs instead of measuring: 'traffic READ_DIR WRITE_DIR' "
                          f"(passes of {' '.join(READ_COUNTERS)} and of {' '.join(WRITE_COUNTERS)}) or 'valu SQ_DIR' "
                          f"(a pass of {' '.join(VALU_COUNTERS)})")
     args = ap.parse_args()
+    only = [k for k in args.only.split(",") if k]
+    if args.trace_child:
+        return trace_child(args.trace_child, args.kernel_rounds, only)
     if args.pmc_summary:
         kind, dirs = args.pmc_summary[0], args.pmc_summary[1:]
         if (kind, len(dirs)) not in (("traffic", 2), ("valu", 1)):
@@ -702,12 +898,14 @@ def main() -> int:
               "(the kernels are per-token; a data-parallel split needs no collectives).", file=sys.stderr)
         return 2
 
-    only = [k for k in args.only.split(",") if k]
-    # The runner's decode steps run first, as child processes, before this
-    # process touches the GPU.
+    # Child processes first, before this process touches the GPU: the
+    # runner's decode steps, then the kernel cases under the kernel tracer.
     decode = None
     if not args.no_decode and not only:
         decode = {f"{n}_sequences": decode_steps(n) for n in (8, 32)}
+    traced, trace_status = {}, "not run"
+    if not args.no_kernels and not args.no_kernel_trace:
+        traced, trace_status = kernel_times(args.kernel_rounds, only)
 
     hip = Hip()
     gpu = nvr.Gpu(0)
@@ -717,7 +915,10 @@ def main() -> int:
     ms = float("nan")
     if not only:
         graph = gpu.capture(chain.step)
+        warm_up(gpu, hip, args.warm_seconds, graph)
         ms = time_graph(gpu, hip, graph, args.steps, args.warmup)
+    else:
+        warm_up(gpu, hip, args.warm_seconds)
     tokens_per_s = args.tokens / (ms / 1e3)
     chain_gbs = chain.bytes() / (ms / 1e3) / 1e9
 
@@ -733,6 +934,11 @@ def main() -> int:
             kernels[name] = {"workload": workload, "us": round(t * 1e3, 3), "bytes": nbytes, "GB/s": round(gbs, 1),
                              "frac": round(gbs / HBM_PEAK_GBS, 4), "rows_per_s": round(rows / (t / 1e3), 1),
                              "launches": len(launches)}
+            if name in traced:
+                kname, kus, n = traced[name]
+                kernels[name].update({"kernel": kname, "kernel_us": round(kus, 3),
+                                      "kernel_frac": round(nbytes / (kus * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                                      "kernel_dispatches": n})
             traffic = measured_traffic(name)
             if traffic is not None:
                 kernels[name]["traffic"] = {"bytes": traffic, "ratio": round(traffic / nbytes, 3),
@@ -743,6 +949,10 @@ def main() -> int:
                 floor_us = valu / (gpu.sm_count() * SCLK_GHZ * 1e3)
                 kernels[name]["valu"] = {"insts": valu, "floor_us": round(floor_us, 2),
                                          "frac": round(floor_us / (t * 1e3), 4), "source": VALU_SUMMARY}
+        for name, tag in (("qkv_rope_8192", "perm of 32 blocks, seed 8192"), ("kv_write_16384", "perm of 128 blocks, seed 7")):
+            if name in kernels:
+                kernels[name]["slot_layout"] = tag
+        fold_layouts(kernels)
 
     # Dominant kernel of the step: the largest share of the step's HBM bytes
     # (launches x algorithmic bytes at the step's shape). By time, SiLU and
@@ -757,6 +967,8 @@ def main() -> int:
         roofline = {"kernel": shape_of[dom], "bound": "hbm", "achieved": kd["GB/s"], "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": kd["frac"], "traffic": measured_traffic(shape_of[dom]),
                     "traffic_source": TRAFFIC_SUMMARY}
+        if "kernel_us" in kd:
+            roofline.update({"kernel_us": kd["kernel_us"], "kernel_frac": kd["kernel_frac"]})
 
     cpu = None
     if not args.no_cpu and not only:
@@ -770,8 +982,13 @@ def main() -> int:
                                "RoPE + paged KV write, add-RMSNorm, SiLU-mul] + final add-RMSNorm, one HIP graph",
                    "tokens": args.tokens, "layers": LAYERS, "hidden": H, "intermediate": I, "q_heads": QH,
                    "kv_heads": KVH, "head_dim": D, "block_size": BS, "parallelism": "none (1 GPU)"},
-        "step_GB/s": round(chain_gbs, 1), "step_hbm_frac": round(chain_gbs / HBM_PEAK_GBS, 4),
-        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels, "decode": decode,
+        "warm_seconds": args.warm_seconds,
+        # Algorithmic bytes over step time. The residual stream and the
+        # per-layer activations the chain rewrites stay in the 256 MB Infinity
+        # Cache between kernels, so this is an effective rate, not HBM traffic.
+        "step_effective_GB/s": round(chain_gbs, 1), "step_effective_frac": round(chain_gbs / HBM_PEAK_GBS, 4),
+        "roofline": roofline, "kernel_time_source": TRACE_NOTE if traced else trace_status,
+        "cpu_baseline": cpu, "kernels": kernels, "decode": decode,
     }
     print(json.dumps(line))
     return 0

@@ -7,6 +7,7 @@ import io
 import os
 import sys
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -96,3 +97,55 @@ def test_committed_summaries_feed_the_benchmark_line():
         assert 0.9 < b / alg[case] < 1.2, (case, b, alg[case])
     for case in ("sampling_256x151936", "sampling_greedy", "sampling_gumbel"):
         assert bench.measured_valu(case) is not None, case
+
+
+def test_kernel_trace_dispatches_are_assigned_to_cases_in_order():
+    """The child runs each case as (warm + rounds) x launches dispatches of one
+    kernel; the timed part's median is the case's kernel time."""
+    order = [{"case": "a", "launches": 2, "warm": 1, "rounds": 3}, {"case": "b", "launches": 1, "warm": 2, "rounds": 3}]
+    disp = []
+    t = 0
+    for dur in [50.0, 50.0] + [10.0, 11.0, 12.0, 13.0, 14.0, 15.0]:  # case a: 2 warm dispatches, 6 timed
+        disp.append((t, dur, "void (anonymous namespace)::ka<1>(int)"))
+        t += 100
+    for dur in [90.0, 90.0, 7.0, 5.0, 6.0]:  # case b: 2 warm, 3 timed
+        disp.append((t, dur, "void kb(float)"))
+        t += 100
+    res, status = bench.assign_dispatches(order, disp[::-1])  # any input order: sorted by start
+    assert status == "ok"
+    assert res["a"] == ("ka<1>", 12.5, 6)
+    assert res["b"] == ("kb", 6.0, 3)
+
+
+@pytest.mark.parametrize("drop,extra", [(1, 0), (0, 1)])
+def test_kernel_trace_that_does_not_line_up_is_refused(drop, extra):
+    order = [{"case": "a", "launches": 1, "warm": 1, "rounds": 2}, {"case": "b", "launches": 1, "warm": 1, "rounds": 2}]
+    disp = [(i, 1.0, "ka") for i in range(3)] + [(10 + i, 1.0, "kb") for i in range(3)]
+    disp = disp[drop:] + [(100 + i, 1.0, "kb") for i in range(extra)]
+    res, status = bench.assign_dispatches(order, disp)
+    assert res == {} and status != "ok"
+
+
+def test_slot_layouts_fold_into_their_case_with_min_and_median():
+    kernels = {"kv": {"us": 20.0, "frac": 0.70, "kernel_us": 19.0, "kernel_frac": 0.74},
+               "kv@identity": {"us": 22.0, "frac": 0.64, "kernel_us": 21.0, "kernel_frac": 0.67},
+               "kv@perm1": {"us": 21.0, "frac": 0.67, "kernel_us": 20.0, "kernel_frac": 0.70},
+               "other": {"us": 1.0, "frac": 0.1}}
+    bench.fold_layouts(kernels)
+    assert set(kernels) == {"kv", "other"}
+    sweep = kernels["kv"]["layout_sweep"]
+    assert sweep["layouts"] == 3
+    assert sweep["frac_min"] == 0.64 and sweep["frac_median"] == 0.67
+    assert sweep["kernel_frac_min"] == 0.67 and sweep["kernel_frac_median"] == 0.70
+    assert kernels["kv"]["layouts"]["identity"]["kernel_us"] == 21.0
+
+
+def test_sweep_slot_layouts_are_distinct_slots_inside_the_cache():
+    for tokens, blocks in ((8192, 32), (16384, 128)):
+        layouts = bench.slot_layouts(tokens, blocks)
+        assert [t for t, _ in layouts] == ["@identity"] + [f"@perm{s}" for s in bench.LAYOUT_SEEDS]
+        for _, slots in layouts:
+            assert len(np.unique(slots)) == tokens
+            assert slots.min() >= 0 and slots.max() < blocks * bench.BS
+            # whole 256-token blocks stay together (slot % 256 == token % 256)
+            assert np.array_equal(slots % bench.BS, np.arange(tokens) % bench.BS)
