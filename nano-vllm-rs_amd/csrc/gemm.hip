@@ -211,11 +211,11 @@ __global__ __launch_bounds__(WAVES * 64) void rms_gemm(const uint16_t* __restric
     }
 }
 
-// Blocks of 8 waves when the grid is at most one block per CU (n <= 4096:
-// more loads in flight per CU, and for 32 rows two passes of the norm
-// instead of four); 4 waves when it is wider, where two smaller blocks per
-// CU (LDS permitting) hide each other's norm.
-constexpr int kCus = 256;
+// Blocks of 8 waves when the grid is at most one block per CU (n <= 4096 on
+// MI355X's 256 CUs: more loads in flight per CU, and for 32 rows two passes
+// of the norm instead of four); 4 waves when it is wider, where two smaller
+// blocks per CU (LDS permitting) hide each other's norm.
+inline int64_t cus_of(const nv_context* c) { return c->cu_count > 0 ? c->cu_count : 256; }
 
 template <int KC, int MT, bool ADD, bool SILU, int WAVES>
 void launch_waves(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_t* res_out, const uint16_t* nw,
@@ -229,7 +229,7 @@ void launch_waves(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_
 template <int KC, int MT, bool ADD, bool SILU>
 void launch(nv_context* c, const uint16_t* x, const uint16_t* res, uint16_t* res_out, const uint16_t* nw,
             const uint16_t* w, uint16_t* y, uint16_t* normed, int m, int n, float eps, uint16_t* act) {
-    if (n / kTileN <= kCus) launch_waves<KC, MT, ADD, SILU, 8>(c, x, res, res_out, nw, w, y, normed, m, n, eps, act);
+    if (n / kTileN <= cus_of(c)) launch_waves<KC, MT, ADD, SILU, 8>(c, x, res, res_out, nw, w, y, normed, m, n, eps, act);
     else launch_waves<KC, MT, ADD, SILU, 4>(c, x, res, res_out, nw, w, y, normed, m, n, eps, act);
 }
 
@@ -421,10 +421,10 @@ int nv_gemm_rows(nv_context* c, const void* x, const void* w, void* y, int m, in
     auto xb = static_cast<const uint16_t*>(x);
     auto wb = static_cast<const uint16_t*>(w);
     auto yb = static_cast<uint16_t*>(y);
-    if (n / kTileN < 256 && m <= 16) {  // too few 16-column tiles to fill the GPU
+    if (n / kTileN < cus_of(c) && m <= 16) {  // too few 16-column tiles to fill the GPU
         if (m <= 8) launch_narrow<8>(c, xb, wb, yb, m, n, k);
         else launch_narrow<16>(c, xb, wb, yb, m, n, k);
-    } else if (n / kTileN >= 256 && k <= 2048) {  // enough tiles to fill the GPU with 4-wave blocks
+    } else if (n / kTileN >= cus_of(c) && k <= 2048) {  // enough tiles to fill the GPU with 4-wave blocks
         if (k == 1024) launch_rows_plain<4, 8>(c, xb, wb, yb, m, n, k);
         else launch_rows_plain<4, 16>(c, xb, wb, yb, m, n, k);
     } else {

@@ -7,6 +7,7 @@
   ownership, overlapping outputs, scalars, head layouts), each rejection by
   the rule it breaks.
 """
+import ctypes
 import os
 import re
 import subprocess
@@ -28,6 +29,97 @@ REFERENCE_SYMBOLS = {
     "nv_rope_cache", "nv_qkv_rope_cached", "nv_attention", "nv_silu", "nv_gather", "nv_sample",
     "nv_sample_parallel",
 }
+
+
+# Argument and return types of every extern the reference's Rust side
+# declares (src/gpu.rs:17-178), transcribed by hand: `*mut c_void` context ->
+# ctx, `*const c_void` -> const void*, `*mut c_void` -> void*,
+# `*mut *mut c_void` -> void**, `*mut c_int` -> int*, `*mut usize` -> size_t*,
+# c_int -> int, f32 -> float, usize -> size_t, `*const c_char` -> const char*.
+_C, _M = "const void*", "void*"
+REFERENCE_EXTERNS = {
+    "nv_stream": ("int", ["ctx", "void**"]),                          # src/gpu.rs:18
+    "nv_sm_count": ("int", ["ctx", "int*"]),                          # :19
+    "nv_last_error": ("const char*", []),                             # :20
+    "nv_create": ("int", ["int", "void**"]),                          # :21
+    "nv_destroy": ("void", ["ctx"]),                                  # :22
+    "nv_alloc": ("int", ["ctx", "size_t", "void**"]),                 # :23
+    "nv_free": ("void", ["ctx", _M]),                                 # :24
+    "nv_upload": ("int", ["ctx", _M, _C, "size_t"]),                  # :25-26
+    "nv_download": ("int", ["ctx", _C, _M, "size_t"]),                # :27-32
+    "nv_sync": ("int", ["ctx"]),                                      # :33
+    "nv_mem_info": ("int", ["ctx", "size_t*", "size_t*"]),            # :34
+    "nv_capture_begin": ("int", ["ctx"]),                             # :35
+    "nv_capture_end": ("int", ["ctx", "void**"]),                     # :36
+    "nv_capture_abort": ("void", ["ctx"]),                            # :37
+    "nv_graph_replay": ("int", ["ctx", _M]),                          # :38
+    "nv_graph_destroy": ("void", ["ctx", _M]),                        # :39
+    "nv_gemm": ("int", ["ctx", _C, _C, _M, "int", "int", "int"]),     # :40-48
+    "nv_embedding": ("int", ["ctx", _C, _C, _M, "int", "int", "int"]),  # :49-57
+    "nv_rms": ("int", ["ctx", _C, _C, _M, "int", "int", "float"]),    # :58-66
+    "nv_add_rms": ("int", ["ctx", _C, _M, _C, _M, "int", "int", "float"]),  # :67-76
+    "nv_qkv_rope": ("int", ["ctx"] + [_C] * 5 + [_M] * 3 + ["int"] * 6 + ["float", "float"]),  # :77-95
+    "nv_rope_cache": ("int", ["ctx", _M, "int", "int", "float"]),     # :96-102
+    "nv_qkv_rope_cached": ("int", ["ctx"] + [_C] * 5 + [_M] * 3 + ["int"] * 6 + ["float", _C, "int"]),  # :103-122
+    "nv_attention": ("int", ["ctx"] + [_C] * 6 + [_M] + ["int"] * 9),  # :123-141
+    "nv_silu": ("int", ["ctx", _C, _M, "int", "int"]),                # :142-148
+    "nv_gather": ("int", ["ctx", _C, _C, _M, "int", "int", "int"]),   # :149-157
+    "nv_sample": ("int", ["ctx", _C, _C, _C, _M, "int", "int"]),      # :158-166
+    "nv_sample_parallel": ("int", ["ctx", _C, _C, _C, _M, _M, _M, "int", "int"]),  # :167-177
+}
+
+
+def header_signatures() -> dict[str, tuple[str, list[str]]]:
+    """{name: (return type, [parameter types])} of every nv_* declaration in the
+    header, parameter names dropped, `nv_context*` written as ctx."""
+    text = re.sub(r"/\*.*?\*/", " ", open(HEADER).read(), flags=re.S)
+    out = {}
+    for ret, name, params in re.findall(r"((?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\**)\s*(nv_[a-z0-9_]+)\s*\(([^)]*)\)\s*;",
+                                        text):
+        types = []
+        for param in [q.strip() for q in params.split(",")]:
+            if param in ("", "void"):
+                continue
+            t = re.sub(r"\s*\b[A-Za-z_][A-Za-z0-9_]*$", "", param)  # drop the parameter name
+            t = re.sub(r"\s*\*", "*", t).strip()
+            types.append({"nv_context*": "ctx", "nv_context**": "void**"}.get(t, t))
+        out[name] = (re.sub(r"\s*\*", "*", ret).strip(), types)
+    return out
+
+
+CTYPE_OF = {"ctx": ctypes.c_void_p, "void*": ctypes.c_void_p, "const void*": ctypes.c_void_p,
+            "void**": ctypes.POINTER(ctypes.c_void_p), "int*": ctypes.POINTER(ctypes.c_int),
+            "size_t*": ctypes.POINTER(ctypes.c_size_t), "int": ctypes.c_int, "float": ctypes.c_float,
+            "size_t": ctypes.c_size_t, "uint64_t": ctypes.c_uint64, "const char*": ctypes.c_char_p, "void": None}
+
+
+def test_header_types_match_the_reference_externs():
+    """Every reference extern keeps its argument count, order and C types
+    (const-ness included) in include/nano_hip.h."""
+    declared = header_signatures()
+    for name, (ret, args) in REFERENCE_EXTERNS.items():
+        assert name in declared, name
+        assert declared[name] == (ret, args), f"{name}: header {declared[name]} != reference {(ret, args)}"
+
+
+def test_wrapper_types_match_the_header():
+    """nvr.SIGNATURES declares each function with the header's C types."""
+    sigs = header_signatures()
+    assert set(sigs) == header_functions() == set(nvr.SIGNATURES)
+    for name, (ret, args) in sigs.items():
+        restype, argtypes = nvr.SIGNATURES[name]
+        assert restype == CTYPE_OF[ret], name
+        assert argtypes == [CTYPE_OF[a] for a in args], name
+
+
+def test_header_signature_parser_sees_a_swapped_argument():
+    """The parser behind the two tests above tells int from float and a
+    pointer from a value (a swapped pair is caught)."""
+    sigs = header_signatures()
+    ret, args = sigs["nv_rope_cache"]
+    assert args == ["ctx", "void*", "int", "int", "float"]
+    assert REFERENCE_EXTERNS["nv_rope_cache"][1] != ["ctx", "void*", "int", "float", "int"]
+    assert sigs["nv_sampling_seed"] == ("uint64_t", ["uint64_t"] * 3)
 
 
 def header_functions() -> set[str]:

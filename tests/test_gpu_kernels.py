@@ -582,6 +582,25 @@ def test_attention_head_dims_groups_and_block_sizes(gpu, dim, qh, kvh, bs):
     _attention_case(gpu, 220 + dim, pos, seqs, qh, kvh, dim, bs, batch, stride, max_context)
 
 
+@pytest.mark.parametrize("dim,qh,kvh,bs", [(256, 4, 4, 64), (256, 4, 4, 256), (64, 8, 2, 256), (32, 4, 2, 64)])
+@pytest.mark.parametrize("above_cus", [False, True])
+def test_attention_aligned_tile_paths_other_head_dims(gpu, dim, qh, kvh, bs, above_cus):
+    """Head dims other than 128 with blocks that hold whole K steps and V
+    tiles: at most one block per CU (V tiles streamed into LDS slots; at head
+    dim 256 a tile is 32 tokens, two rows per 1 KB wave load) and more blocks
+    than CUs (V tiles through registers); contexts ending on and inside
+    tiles."""
+    cus = gpu.sm_count()
+    rows = cus // qh + 1 if above_cus else min(9, cus // qh)
+    batch, max_context = 4, 520
+    stride = -(-max_context // bs)
+    rng = np.random.default_rng(dim * 11 + bs + above_cus)
+    pos = rng.integers(0, max_context, size=rows)
+    pos[:5] = [max_context - 1, 31, 32, 63, 0]
+    seqs = rng.integers(0, batch, size=rows)
+    _attention_case(gpu, 270 + dim + bs + above_cus, pos, seqs, qh, kvh, dim, bs, batch, stride, max_context)
+
+
 def test_attention_invalid_rows_and_blocks(gpu):
     """Rows with a bad sequence index or a context beyond max_context or the
     table give zeros; table entries outside [0, blocks) drop their tokens."""

@@ -53,3 +53,25 @@ def test_static_partials_limit_is_refused():
     ok = nvr.Gpu.STATIC_PARTIALS // 75
     gpu.sample_parallel_static(lb, tb, sb, ob, ok, vocab)
     gpu.sync()
+
+
+def test_static_partials_filled_to_the_limit():
+    """A batch that fills the static array exactly (16 rows of 8192 partitions
+    of 2048 tokens: 131072 partials, written by the one-pass partition path),
+    each row's winner planted in its last partition so the top entries of
+    both halves of the array decide the result; then a smaller call."""
+    gpu = nvr.Gpu(0)
+    batch, vocab = 16, 8191 * 2048 + 8
+    assert batch * -(-vocab // 2048) == nvr.Gpu.STATIC_PARTIALS
+    print(f"static sampler at the limit: batch {batch}, vocab {vocab}", flush=True)
+    logits = np.random.default_rng(950).integers(0x3C00, 0x4000, size=(batch, vocab), dtype=np.uint16)
+    planted = vocab - 1 - 37 * np.arange(batch)
+    logits[np.arange(batch), planted] = 0x4300  # 128.0: wins greedy and Gumbel (T = 0.6) rows alike
+    temps = np.array([0.0, 0.6] * (batch // 2), np.float32)
+    seeds = np.array([ora.sampling_seed(950, r, r) for r in range(batch)], np.uint64)
+    got_scratch, got_static = _both(gpu, logits, temps, seeds, batch, vocab)
+    del logits
+    assert got_static.tolist() == got_scratch.tolist() == planted.tolist()
+    small, temps2, seeds2 = _batch(3, 151936, 951)
+    got_scratch, got_static = _both(gpu, small, temps2, seeds2, 3, 151936)
+    assert got_static.tolist() == got_scratch.tolist() == ora.sample(small, temps2, seeds2, 3, 151936).tolist()
