@@ -14,6 +14,9 @@ struct nv_context {
     // Device address of this device's copy of the sampler's static partials
     // (sample.hip), for nv_sample_parallel_static.
     void* static_partials;
+    // The paired sampler's per-row exchange words (sample.hip): two uint64
+    // per row, zero between launches (every launch leaves them zero).
+    void* pair_state;
 };
 
 namespace nvr {
@@ -27,6 +30,10 @@ int fail(int code, const char* fmt, ...);
 // Looks up this device's copy of the sampler's static partials (called by
 // nv_create with the context's device current).
 int bind_static_partials(nv_context* c);
+
+// Allocates and zeroes the paired sampler's exchange words (nv_create);
+// released by nv_destroy.
+int create_pair_state(nv_context* c);
 
 // Status of the most recent launch on this thread.
 inline int launch_status() { return hip_status(hipGetLastError(), "HIP kernel launch"); }

@@ -71,7 +71,7 @@ int nv_sm_count(nv_context* c, int* output) {
 
 int nv_create(int device, nv_context** output) {
     NVR_HIP(hipSetDevice(device));
-    nv_context* c = new (std::nothrow) nv_context{device, nullptr, nullptr, 0, nullptr};
+    nv_context* c = new (std::nothrow) nv_context{device, nullptr, nullptr, 0, nullptr, nullptr};
     if (!c) return nvr::fail(-1, "host context allocation failed");
     int error = nvr::hip_status(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking),
                                 "hipStreamCreateWithFlags");
@@ -87,7 +87,14 @@ int nv_create(int device, nv_context** output) {
     if (!error) error = nvr::blas_status(hipblasSetAtomicsMode(c->blas, HIPBLAS_ATOMICS_NOT_ALLOWED),
                                          "hipblasSetAtomicsMode");
     if (!error) error = nvr::bind_static_partials(c);
-    if (error) { hipblasDestroy(c->blas); (void)hipStreamDestroy(c->stream); delete c; return error; }
+    if (!error) error = nvr::create_pair_state(c);
+    if (error) {
+        if (c->pair_state) (void)hipFree(c->pair_state);
+        hipblasDestroy(c->blas);
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return error;
+    }
     *output = c;
     return 0;
 }
@@ -96,6 +103,7 @@ void nv_destroy(nv_context* c) {
     if (!c) return;
     (void)hipSetDevice(c->device);
     (void)hipStreamSynchronize(c->stream);
+    if (c->pair_state) (void)hipFree(c->pair_state);
     hipblasDestroy(c->blas);
     (void)hipStreamDestroy(c->stream);
     delete c;

@@ -403,16 +403,17 @@ __device__ __forceinline__ float score_from_m(float logit, float temperature, ui
     return logit / temperature - nvr::nvr_logf(-nvr::nvr_logf(u));
 }
 
-// Scores a wave's queue entries [lane, count), two per lane per iteration (an
-// odd tail scores one entry twice). Entry = f32 bits of the logit (low 16 bits
+// Scores queue entries [begin, count), two per lane per iteration (an odd
+// tail scores one entry twice). Entry = f32 bits of the logit (low 16 bits
 // zero) | chunk round k << 9 | lane << 3 | element; chunk = k * stride + base +
-// lane, base being the wave's first chunk of round 0. TAB: the hash floor of a
-// logit is read from xfloors, indexed by its bf16 bits minus lxb, instead of
-// computed.
+// lane, base being the compacting wave's first chunk of round 0. TAB: the
+// hash floor of a logit is read from xfloors, indexed by its bf16 bits minus
+// lxb, instead of computed.
 template <bool TAB>
-__device__ __forceinline__ void score_queue(const uint32_t* queue, int count, int lane, int base, int stride,
-                                            const Pruner& p, const uint32_t* xfloors, int lxb, Best& best) {
-    for (int j = lane; j < count; j += 2 * kWave) {
+__device__ __forceinline__ void score_queue(const uint32_t* queue, int begin, int count, int lane, int base,
+                                            int stride, const Pruner& p, const uint32_t* xfloors, int lxb,
+                                            Best& best) {
+    for (int j = begin + lane; j < count; j += 2 * kWave) {
         const uint32_t e0 = queue[j];
         const uint32_t e1 = queue[j + kWave < count ? j + kWave : j];
         // Chunk k * stride + base + lane (k < 32 and stride, base below 2^24:
@@ -449,6 +450,163 @@ __device__ __forceinline__ Best block_fold(Best b, float* scores, int* ids) {
 #pragma unroll
     for (int w = 1; w < W; ++w) consider(r, scores[w], ids[w]);
     return r;
+}
+
+// Phase 1 of the resident samplers, as the chunks arrive: the lane's best
+// chunk under "higher maximum wins; an equal maximum only while there is
+// none" (the lane sees its tokens in increasing order, so that keeps the
+// lowest index, and a lane of -inf logits picks its first chunk), then the
+// lowest token of that chunk holding the maximum. Chunk k of the lane is
+// k * stride + first; chunks past the row end become NaN, which fmaxf skips
+// and which never wins or becomes a candidate. Branch-free.
+constexpr uint32_t kNaN2 = 0x7fc07fc0u;
+template <int C>
+__device__ __forceinline__ Best lane_best(uint4 (&w)[C], int stride, int first, int chunks) {
+    float bv = -__builtin_inff();
+    int bk = -1;
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        const bool valid = k * stride + first < chunks;
+        w[k].x = valid ? w[k].x : kNaN2;
+        w[k].y = valid ? w[k].y : kNaN2;
+        w[k].z = valid ? w[k].z : kNaN2;
+        w[k].w = valid ? w[k].w : kNaN2;
+        float f[8];
+        nvr::unpack8(w[k], f);
+        const float m = fmaxf(fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3])), fmaxf(fmaxf(f[4], f[5]), fmaxf(f[6], f[7])));
+        const bool take = (m > bv) | ((bk < 0) & (m == bv));
+        bv = take ? m : bv;
+        bk = take ? k : bk;
+    }
+    // The lowest token of the best chunk holding bv (select over the chunks,
+    // no dynamic register indexing).
+    uint4 bw = make_uint4(kNaN2, kNaN2, kNaN2, kNaN2);
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        bw.x = bk == k ? w[k].x : bw.x;
+        bw.y = bk == k ? w[k].y : bw.y;
+        bw.z = bk == k ? w[k].z : bw.z;
+        bw.w = bk == k ? w[k].w : bw.w;
+    }
+    Best lb{bv, nvr::kNoIndex};
+    float f[8];
+    nvr::unpack8(bw, f);
+    int e = 8;
+#pragma unroll
+    for (int i = 7; i >= 0; --i) e = f[i] == bv ? i : e;
+    if (bk >= 0) lb.index = 8 * (bk * stride + first) + e;
+    // Keep only the packed words live into the later phases (without this the
+    // compiler keeps the unpacked floats instead, twice the registers).
+#pragma unroll
+    for (int k = 0; k < C; ++k) __asm__ volatile("" : "+v"(w[k].x), "+v"(w[k].y), "+v"(w[k].z), "+v"(w[k].w));
+    return lb;
+}
+
+// The candidates of a Gumbel row pruned against s0 are exactly the logits
+// x >= lx, lx the smallest bf16 value with x * (1/T) >= (s0 - kNoiseMax) -
+// (|s0| + 34) * 2^-17 (x * (1/T) is nondecreasing in x; the margin covers
+// 1/T's and the score's roundings): a binary search over the order-preserving
+// 16-bit keys of the bf16 values (-inf .. +inf). -inf when pruning is off.
+__device__ __forceinline__ float candidate_floor(float s0, float inv_t, bool on) {
+    if (!on) return -__builtin_inff();
+    const float bound = (s0 - kNoiseMax) - (__builtin_fabsf(s0) + 34.0f) * 0x1.0p-17f;
+    auto value = [](int key) { return nvr::bf16_to_f32(uint16_t(key >= 0x8000 ? key - 0x8000 : 0xffff - key)); };
+    int lo = 0x007f, hi = 0xff80;  // -inf, +inf; +inf always qualifies
+    if (value(lo) * inv_t >= bound) hi = lo;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (value(mid) * inv_t >= bound) hi = mid;
+        else lo = mid;
+    }
+    return value(hi);
+}
+
+// One window of a wave's compaction: the candidates (x >= lx) of the lane's
+// chunks, in chunk and element order across the wave, from queue position
+// `window` on, at most `capacity` of them (ballot + mbcnt). Entry = f32 bits
+// of the logit (low 16 bits zero) | chunk round k << 9 | lane << 3 |
+// element. Returns the wave's candidate count minus `window`.
+template <int C>
+__device__ __forceinline__ int compact_window(uint4 (&w)[C], float lx, uint32_t* queue, int window, int capacity,
+                                              uint32_t lane_code) {
+    int n = -window;  // queue position of the next candidate
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        // Opaque per window, so the compiler recomputes the keys from the
+        // packed words instead of hoisting 8 C of them out of the loop.
+        __asm__ volatile("" : "+v"(w[k].x), "+v"(w[k].y), "+v"(w[k].z), "+v"(w[k].w));
+        const uint32_t words[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t xb = (i & 1) ? (words[i / 2] & 0xffff0000u) : (words[i / 2] << 16);
+            const bool take = __uint_as_float(xb) >= lx;
+            const uint64_t ballot = __ballot(take);
+            const uint32_t pos = __builtin_amdgcn_mbcnt_hi(uint32_t(ballot >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), uint32_t(n)));
+            if (take & (pos < uint32_t(capacity))) queue[pos] = xb | lane_code | uint32_t(k << 9 | i);
+            n += int(__popcll(ballot));
+        }
+    }
+    return n;
+}
+
+// compact_window for waves that run two to a SIMD, with the same entries
+// in the same order: a chunk's eight ballots are taken before any position,
+// and every lane stores for every element, so no store needs an exec mask
+// and no element waits on the previous one's scalar count. The queue holds
+// `capacity` entries followed by one spare per lane; a non-candidate stores
+// into its lane's spare, a candidate past the window into min(position,
+// capacity + lane), a spare too (each of those slots holds junk).
+template <int C>
+__device__ __forceinline__ int compact_window_dense(uint4 (&w)[C], float lx, uint32_t* queue, int window,
+                                                    int capacity, uint32_t lane_code) {
+    const uint32_t spare = uint32_t(capacity) + (lane_code >> 3);
+    int n = -window;
+#pragma unroll
+    for (int k = 0; k < C; ++k) {
+        __asm__ volatile("" : "+v"(w[k].x), "+v"(w[k].y), "+v"(w[k].z), "+v"(w[k].w));
+        const uint32_t words[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
+        uint32_t xb[8];
+        uint64_t bal[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            xb[i] = (i & 1) ? (words[i / 2] & 0xffff0000u) : (words[i / 2] << 16);
+            bal[i] = __ballot(__uint_as_float(xb[i]) >= lx);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t pos = __builtin_amdgcn_mbcnt_hi(uint32_t(bal[i] >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo(uint32_t(bal[i]), uint32_t(n)));
+            // the ballot is the candidate lanes' mask: select on it directly
+            // (as a plain select the compiler masks exec around the position)
+            uint32_t to;
+            __asm__("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(to) : "v"(spare), "v"(min(pos, spare)), "s"(bal[i]));
+            queue[to] = xb[i] | lane_code | uint32_t(k << 9 | i);
+            n += int(__popcll(bal[i]));
+        }
+    }
+    return n;
+}
+
+// Most tokens are candidates (high temperature, flat rows): queue windows
+// would cost more than they save, so every lane scores its own candidates,
+// re-reading its chunks k * stride + first (cache hits).
+__device__ __forceinline__ void score_in_place(const uint16_t* row, int first, int stride, int chunks, float lx,
+                                               const Pruner& p, Best& best) {
+    const uint32_t* words = reinterpret_cast<const uint32_t*>(row);
+#pragma unroll 1
+    for (int c = first; c < chunks; c += stride) {
+        const uint4 v = *reinterpret_cast<const uint4*>(words + 4 * c);
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float x = __uint_as_float((i & 1) ? (vw[i / 2] & 0xffff0000u) : (vw[i / 2] << 16));
+            if (x >= lx) {
+                const uint32_t f = hash_floor(p, x), m = hash_m(p.seed, uint32_t(8 * c + i));
+                if (m >= f) consider(best, score_from_m(x, p.temperature, m), 8 * c + i);
+            }
+        }
+    }
 }
 
 // One row (parts == 1) or one half of a row (parts == 2) per block, resident
@@ -507,51 +665,7 @@ __global__ __launch_bounds__(TPB) void sample_resident(const uint16_t* __restric
     if (gumbel)
         for (int k = tid; k < kFloorSteps; k += TPB) floors[k] = noise_floor(k);
 
-    // Phase 1, as the chunks arrive: the lane's best chunk under "higher
-    // maximum wins; an equal maximum only while there is none" (the lane sees
-    // its tokens in increasing order, so that keeps the lowest index, and a
-    // lane of -inf logits picks its first chunk). Chunks past the row end
-    // become NaN, which fmaxf skips and which never wins. Branch-free.
-    constexpr uint32_t kNaN2 = 0x7fc07fc0u;
-    float bv = -__builtin_inff();
-    int bk = -1;
-#pragma unroll
-    for (int k = 0; k < C; ++k) {
-        const bool valid = k * stride + first < chunks;
-        w[k].x = valid ? w[k].x : kNaN2;
-        w[k].y = valid ? w[k].y : kNaN2;
-        w[k].z = valid ? w[k].z : kNaN2;
-        w[k].w = valid ? w[k].w : kNaN2;
-        float f[8];
-        nvr::unpack8(w[k], f);
-        const float m = fmaxf(fmaxf(fmaxf(f[0], f[1]), fmaxf(f[2], f[3])), fmaxf(fmaxf(f[4], f[5]), fmaxf(f[6], f[7])));
-        const bool take = (m > bv) | ((bk < 0) & (m == bv));
-        bv = take ? m : bv;
-        bk = take ? k : bk;
-    }
-    // The lowest token of the best chunk holding bv (select over the chunks,
-    // no dynamic register indexing).
-    uint4 bw = make_uint4(kNaN2, kNaN2, kNaN2, kNaN2);
-#pragma unroll
-    for (int k = 0; k < C; ++k) {
-        bw.x = bk == k ? w[k].x : bw.x;
-        bw.y = bk == k ? w[k].y : bw.y;
-        bw.z = bk == k ? w[k].z : bw.z;
-        bw.w = bk == k ? w[k].w : bw.w;
-    }
-    Best lb{bv, nvr::kNoIndex};
-    {
-        float f[8];
-        nvr::unpack8(bw, f);
-        int e = 8;
-#pragma unroll
-        for (int i = 7; i >= 0; --i) e = f[i] == bv ? i : e;
-        if (bk >= 0) lb.index = 8 * (bk * stride + first) + e;
-    }
-    // Keep only the packed words live into phase 3 (without this the compiler
-    // keeps phase 1's unpacked floats instead, twice the registers).
-#pragma unroll
-    for (int k = 0; k < C; ++k) __asm__ volatile("" : "+v"(w[k].x), "+v"(w[k].y), "+v"(w[k].z), "+v"(w[k].w));
+    const Best lb = lane_best<C>(w, stride, first, chunks);
     const Best top = block_fold<kW>(lb, fold_s, fold_i);
     if (!gumbel) {
         finish(top);
@@ -564,22 +678,7 @@ __global__ __launch_bounds__(TPB) void sample_resident(const uint16_t* __restric
     const Best seeded = block_fold<kW>(own, fold_s + kW, fold_i + kW);
     const float s0 = seeded.score, inv_t = 1.0f / temperature;
     const bool on = __builtin_fabsf(s0) < __builtin_inff() && inv_t < __builtin_inff();
-    const float bound = on ? (s0 - kNoiseMax) - (__builtin_fabsf(s0) + 34.0f) * 0x1.0p-17f : -__builtin_inff();
-    // The candidates are exactly the logits x >= lx, lx the smallest bf16 value
-    // with x * (1/T) >= bound (x * (1/T) is nondecreasing in x): a binary search
-    // over the order-preserving 16-bit keys of the bf16 values (-inf .. +inf).
-    float lx = -__builtin_inff();
-    if (on) {
-        auto value = [](int key) { return nvr::bf16_to_f32(uint16_t(key >= 0x8000 ? key - 0x8000 : 0xffff - key)); };
-        int lo = 0x007f, hi = 0xff80;  // -inf, +inf; +inf always qualifies
-        if (value(lo) * inv_t >= bound) hi = lo;
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (value(mid) * inv_t >= bound) hi = mid;
-            else lo = mid;
-        }
-        lx = value(hi);
-    }
+    const float lx = candidate_floor(s0, inv_t, on);
 
     // Phase 3: each wave compacts its candidates into its LDS queue (ballot +
     // mbcnt) and scores them, in rounds of kQ entries when there are
@@ -605,50 +704,17 @@ __global__ __launch_bounds__(TPB) void sample_resident(const uint16_t* __restric
         __syncthreads();
     }
     for (int window = 0;; window += kQ) {
-        int n = -window;  // queue position of the next candidate
-#pragma unroll
-        for (int k = 0; k < C; ++k) {
-            // Opaque per round, so the compiler recomputes the keys from the
-            // packed words instead of hoisting 8 C of them out of the loop.
-            __asm__ volatile("" : "+v"(w[k].x), "+v"(w[k].y), "+v"(w[k].z), "+v"(w[k].w));
-            const uint32_t words[4] = {w[k].x, w[k].y, w[k].z, w[k].w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t xb = (i & 1) ? (words[i / 2] & 0xffff0000u) : (words[i / 2] << 16);
-                const bool take = __uint_as_float(xb) >= lx;
-                const uint64_t ballot = __ballot(take);
-                const uint32_t pos = __builtin_amdgcn_mbcnt_hi(uint32_t(ballot >> 32),
-                                                               __builtin_amdgcn_mbcnt_lo(uint32_t(ballot), uint32_t(n)));
-                if (take & (pos < uint32_t(kQ))) queue[pos] = xb | lane_code | uint32_t(k << 9 | i);
-                n += int(__popcll(ballot));
-            }
-        }
+        const int n = compact_window<C>(w, lx, queue, window, kQ, lane_code);
         if (window == 0 && n > 2 * kQ) {
-            // Most tokens are candidates (high temperature, flat rows): queue
-            // rounds would cost more than they save, so every lane scores its
-            // own candidates, re-reading its chunks (cache hits).
-            const uint32_t* words = reinterpret_cast<const uint32_t*>(row);
-#pragma unroll 1
-            for (int c = first; c < chunks; c += stride) {
-                const uint4 v = *reinterpret_cast<const uint4*>(words + 4 * c);
-                const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const float x = __uint_as_float((i & 1) ? (vw[i / 2] & 0xffff0000u) : (vw[i / 2] << 16));
-                    if (x >= lx) {
-                        const uint32_t f = hash_floor(p, x), m = hash_m(seed, uint32_t(8 * c + i));
-                        if (m >= f) consider(best, score_from_m(x, temperature, m), 8 * c + i);
-                    }
-                }
-            }
+            score_in_place(row, first, stride, chunks, lx, p, best);
             break;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const int count = min(n, kQ);
-        if (tab) score_queue<true>(queue, count, lane, base, stride, p, xfloors, lxb, best);
-        else score_queue<false>(queue, count, lane, base, stride, p, xfloors, lxb, best);
+        if (tab) score_queue<true>(queue, 0, count, lane, base, stride, p, xfloors, lxb, best);
+        else score_queue<false>(queue, 0, count, lane, base, stride, p, xfloors, lxb, best);
         if (n <= kQ) break;
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -656,6 +722,321 @@ __global__ __launch_bounds__(TPB) void sample_resident(const uint16_t* __restric
     }
     best = block_fold<kW>(best, fold_s + 2 * kW, fold_i + 2 * kW);
     finish(best);
+}
+
+// ------------------------------------------------------- paired halves ----
+// One 1024-thread block per row, like sample_resident, but each block holds
+// two half rows: waves 0-7 (slot 0) take half 0 of row b = blockIdx.x and
+// waves 8-15 (slot 1) half 1 of row partner_row(b). Half h of a row is its
+// chunks k * 1024 + 512 h + t (t < 512, k < C). Partners pair each Gumbel
+// row (T > 0) with a greedy row, so with one row per CU a mixed batch puts
+// half a Gumbel row and half a greedy row on every CU instead of a whole
+// Gumbel row on half of them: once the greedy half is done (its maximum
+// needs no second pass), its waves score the back halves of the Gumbel
+// half's candidate queues. Rows left without a partner hold both halves in
+// one block, which then works as sample_resident does.
+//
+// A row split over two blocks needs two exchanges, through the context's
+// per-row words (two uint64, zero between launches): X, the halves' s0 (the
+// best exact score of their lane maxima), each half ORing its order key into
+// its 32 bits and waiting a bounded time for the other's, so that both prune
+// against the better s0 (a real token's score, so pruning stays exact); and
+// Y, the halves' (score, index) keys met in a 64-bit atomic maximum, whose
+// returned value tells the second half that it holds both: it writes the
+// token and zeroes X and Y. A half that waits in vain (its partner's block
+// not yet resident, when rows outnumber CUs) prunes against its own s0.
+constexpr int kPairThreads = 1024, kPairWaves = 16, kSlotThreads = 512, kSlotWaves = 8;
+constexpr int kPairQueue = 2304;   // queue entries per wave: kPairCap, then a spare per lane
+constexpr int kPairCap = kPairQueue - kWave;
+constexpr int kPairRows = 16384;   // rows of the context's exchange words
+constexpr int kPairWaitTicks = 400;  // 4 us of the 100 MHz realtime counter
+constexpr size_t kPairLdsBytes =
+    sizeof(uint32_t) * (size_t(kPairWaves) * kPairQueue + kFloorSteps + 2 * kXFloors) +
+    3 * kPairWaves * (sizeof(float) + sizeof(int)) + kPairWaves * sizeof(int) + 2 * sizeof(float) + sizeof(int);
+static_assert(kPairLdsBytes <= 160 * 1024, "the paired sampler's block must fit one CU's LDS");
+
+// Order key of a score for the exchanges: increasing in the score, -0 and +0
+// equal, at least 0x007fffff (-inf) for every non-NaN score, so 0 means absent.
+__device__ __forceinline__ uint32_t score_key(float s) {
+    const uint32_t u = __float_as_uint(s == 0.0f ? 0.0f : s);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_score(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+// (score, index) as one key ordered like `better`: higher score, then lower
+// index. "No winner" is the smallest key that is not zero.
+__device__ __forceinline__ uint64_t result_key(const Best& b) {
+    if (b.index == nvr::kNoIndex) return uint64_t(1) << 32;
+    return (uint64_t(score_key(b.score)) << 32) | uint32_t(0x7fffffff - b.index);
+}
+
+// The row whose half 1 block b's slot 1 holds: the k-th Gumbel row and the
+// k-th greedy row (in row order) are partners; rows beyond the shorter list
+// are their own partners. partner_row(partner_row(b)) == b, so every half is
+// taken once. Wave-uniform; every lane of the wave takes part. Up to
+// 64 * kDealLoads rows it works on temperatures loaded by load_deal, which
+// the kernel issues before any logit load of the block: behind those (152 KB
+// per CU) a load would wait for the CU's share of the memory bandwidth.
+constexpr int kDealLoads = 16;
+struct DealTemps {
+    float t[kDealLoads];  // temps[64 c + lane] (clamped to the last row)
+    float own;            // temps[b]
+};
+__device__ __forceinline__ DealTemps load_deal(const float* temps, int batch, int b, int lane) {
+    DealTemps d;
+    d.own = temps[b];
+#pragma unroll
+    for (int c = 0; c < kDealLoads; ++c) d.t[c] = temps[min(c * kWave + lane, batch - 1)];
+    return d;
+}
+__device__ __forceinline__ int partner_row(const float* temps, const DealTemps& d, int batch, int b, int lane) {
+    const bool gum = d.own > 0.0f;
+    const bool one_round = batch <= kWave * kDealLoads;
+    uint64_t kinds[kDealLoads];  // bit l of kinds[c]: row 64 c + l is Gumbel
+#pragma unroll
+    for (int c = 0; c < kDealLoads; ++c) kinds[c] = __ballot(c * kWave + lane < batch && d.t[c] > 0.0f);
+    auto kind_mask = [&](int c) {  // Gumbel rows among 64 c .. 64 c + 63
+        if (one_round) {
+            uint64_t m = 0;
+#pragma unroll
+            for (int k = 0; k < kDealLoads; ++k) m = k == c ? kinds[k] : m;
+            return m;
+        }
+        const int i = c * kWave + lane;
+        return uint64_t(__ballot(i < batch && temps[i] > 0.0f));
+    };
+    const int nc = (batch + kWave - 1) / kWave;
+    int before = 0, total = 0;  // Gumbel rows before b, and in all
+    for (int c = 0; c < nc; ++c) {
+        const uint64_t g = kind_mask(c);
+        total += __popcll(g);
+        const int off = b - c * kWave;
+        if (off >= 0) before += __popcll(off >= kWave ? g : g & ((uint64_t(1) << off) - 1));
+    }
+    const int rank = gum ? before : b - before;
+    if (rank >= (gum ? batch - total : total)) return b;
+    int seen = 0;
+    for (int c = 0; c < nc; ++c) {
+        const uint64_t valid = c * kWave + kWave <= batch ? ~uint64_t(0) : (uint64_t(1) << (batch - c * kWave)) - 1;
+        uint64_t m = (gum ? ~kind_mask(c) : kind_mask(c)) & valid;  // rows of the other kind
+        const int n = __popcll(m);
+        if (rank < seen + n) {
+            for (int k = rank - seen; k > 0; --k) m &= m - 1;
+            return c * kWave + __builtin_ctzll(m);
+        }
+        seen += n;
+    }
+    return b;
+}
+
+// Best over waves [w0, w0 + n) of a fold array.
+__device__ __forceinline__ Best fold_waves(const float* s, const int* i, int w0, int n) {
+    Best r{s[w0], i[w0]};
+    for (int w = 1; w < n; ++w) consider(r, s[w0 + w], i[w0 + w]);
+    return r;
+}
+
+// X exchange of half `half` of row r (one thread): publish s0's key, wait for
+// the other half's, return the better of the two.
+__device__ __forceinline__ float exchange_s0(uint64_t* state, int r, int half, float s0) {
+    uint64_t* x = state + 2 * int64_t(r);
+    const uint64_t old = __hip_atomic_fetch_or(x, uint64_t(score_key(s0)) << (32 * half), __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t other = uint32_t(old >> (32 * (1 - half)));
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (other == 0 && int64_t(__builtin_amdgcn_s_memrealtime() - t0) < kPairWaitTicks) {
+        __builtin_amdgcn_s_sleep(1);
+        other = uint32_t(__hip_atomic_load(x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> (32 * (1 - half)));
+    }
+    return other != 0 ? fmaxf(s0, key_score(other)) : s0;
+}
+
+// Y exchange (one thread): meet the other half's result; the second half to
+// arrive writes the token and leaves both words zero for the next launch.
+// `seen` is a value of Y read earlier by this half: when it already holds
+// the other half's key, this half is the second without another atomic.
+__device__ __forceinline__ void deposit(uint64_t* state, int r, const Best& b, int* out, uint64_t seen = 0) {
+    uint64_t* x = state + 2 * int64_t(r);
+    const uint64_t key = result_key(b);
+    const uint64_t old =
+        seen != 0 ? seen : __hip_atomic_fetch_max(x + 1, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == 0) return;
+    const uint64_t m = old > key ? old : key;
+    out[r] = (m >> 32) == 1 ? 0 : int(0x7fffffff - uint32_t(m));
+    __hip_atomic_store(x + 1, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(x, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Queue entries [0, split(n)) are scored by their compacting wave, the rest
+// by its helper in the other slot (a multiple of two entries per lane).
+__device__ __forceinline__ int helper_split(int n) { return min(n, (n + 4 * kWave - 1) / (4 * kWave) * (2 * kWave)); }
+
+template <int C>
+__global__ __launch_bounds__(kPairThreads) void sample_paired(const uint16_t* __restrict__ logits,
+                                                             const float* __restrict__ temps,
+                                                             const uint64_t* __restrict__ seeds,
+                                                             int* __restrict__ out, uint64_t* __restrict__ state,
+                                                             int vocab, int batch) {
+    constexpr int kQ = kPairQueue, kCap = kPairCap, stride = 2 * kSlotThreads;
+    extern __shared__ __align__(16) uint32_t lds[];
+    uint32_t* floors = lds + kPairWaves * kQ;
+    uint32_t* xfloors = floors + kFloorSteps;                            // [2][kXFloors]
+    float* fold_s = reinterpret_cast<float*>(xfloors + 2 * kXFloors);    // [3][kPairWaves]
+    int* fold_i = reinterpret_cast<int*>(fold_s + 3 * kPairWaves);       // [3][kPairWaves]
+    int* counts = fold_i + 3 * kPairWaves;                               // [kPairWaves]
+    float* slot_s0 = reinterpret_cast<float*>(counts + kPairWaves);      // [2]
+    int* slot1_row = reinterpret_cast<int*>(slot_s0 + 2);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int slot = wave / kSlotWaves, sw = wave % kSlotWaves, st = tid % kSlotThreads;
+    const int b = blockIdx.x;
+    // Slot 1's temperature loads go out before any logit load of the block
+    // (the barrier orders the issue only: no memory fence, nothing waits).
+    DealTemps deal;
+    if (slot == 1) deal = load_deal(temps, batch, b, lane);
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+    if (slot == 1) {  // opaque after the barrier: the wait for the loads stays on slot 1's side of it
+#pragma unroll
+        for (int c = 0; c < kDealLoads; ++c) __asm__ volatile("" : "+v"(deal.t[c]));
+        __asm__ volatile("" : "+v"(deal.own));
+    }
+    const int r = slot == 0 ? b : __builtin_amdgcn_readfirstlane(partner_row(temps, deal, batch, b, lane));
+    const int chunks = vocab / 8;
+    const int first = slot * kSlotThreads + st;
+    const uint16_t* row = logits + int64_t(r) * vocab;
+    uint4 w[C];
+#pragma unroll
+    for (int k = 0; k < C; ++k) w[k] = nvr::load_stream(row + 8 * int64_t(min(k * stride + first, chunks - 1)));
+    const float temperature = temps[r];
+    const uint64_t seed = seeds[r];
+    const bool gumbel = temperature > 0.0f;
+    for (int k = tid; k < kFloorSteps; k += kPairThreads) floors[k] = noise_floor(k);
+    if (tid == kSlotThreads) *slot1_row = r;
+
+    // Phase 1: lane maxima; each slot's greedy maximum. Phase 2 (Gumbel
+    // halves): every lane scores its maximum's token exactly; the best of
+    // those real scores is the half's s0 (folded after the same barrier, while
+    // an early slot waits for the other).
+    const Best lb = lane_best<C>(w, stride, first, chunks);
+    {
+        const Best wb = wave_argmax(lb);
+        if (lane == 0) { fold_s[wave] = wb.score; fold_i[wave] = wb.index; }
+        Best own{-__builtin_inff(), nvr::kNoIndex};
+        if (gumbel && lb.index != nvr::kNoIndex)
+            own = Best{nvr::gumbel_score(lb.score, temperature, seed, uint32_t(lb.index)), lb.index};
+        own = wave_argmax(own);
+        if (lane == 0) { fold_s[kPairWaves + wave] = own.score; fold_i[kPairWaves + wave] = own.index; }
+    }
+    __syncthreads();
+    const int r1 = *slot1_row;
+    const bool whole = r1 == b;  // both halves of row b in this block
+    const Best top = whole ? fold_waves(fold_s, fold_i, 0, kPairWaves)
+                           : fold_waves(fold_s, fold_i, slot * kSlotWaves, kSlotWaves);
+    if (!gumbel) {
+        if (whole) {  // a whole greedy row: done (every wave of the block leaves here)
+            if (tid == 0) out[r] = top.index == nvr::kNoIndex ? 0 : top.index;
+            return;
+        }
+        if (st == 0) deposit(state, r, top, out);
+    }
+
+    // s0 of the half (or of the row); a split Gumbel row trades its halves'.
+    const Best seeded = whole ? fold_waves(fold_s + kPairWaves, fold_i + kPairWaves, 0, kPairWaves)
+                              : fold_waves(fold_s + kPairWaves, fold_i + kPairWaves, slot * kSlotWaves, kSlotWaves);
+    // A split Gumbel half reads Y once its s0 is settled: its greedy partner
+    // has usually deposited by then, and the read's round trip overlaps the
+    // compaction instead of ending the launch.
+    uint64_t partner_key = 0;
+    if (gumbel && !whole && st == 0) {
+        slot_s0[slot] = exchange_s0(state, r, slot, seeded.score);
+        partner_key = __hip_atomic_load(state + 2 * int64_t(r) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+
+    // The Gumbel half whose queues this wave compacts or helps score: its own
+    // slot, or (a greedy half split from a Gumbel row's) the other slot.
+    const int gslot = gumbel || whole ? slot : 1 - slot;
+    const bool helps = !gumbel && !whole && (temps[slot == 0 ? r1 : b] > 0.0f);
+    const int grow = gslot == 0 ? b : r1;
+    const float gt = gumbel ? temperature : temps[grow];
+    const uint64_t gseed = gumbel ? seed : seeds[grow];
+    const float s0 = whole ? seeded.score : slot_s0[gslot];
+    const float inv_t = 1.0f / gt;
+    const bool on = __builtin_fabsf(s0) < __builtin_inff() && inv_t < __builtin_inff();
+    const float lx = candidate_floor(s0, inv_t, on);
+    const Pruner p{s0, inv_t, gt, gseed, on, floors};
+    // Tabulated hash floors over the candidate values [lx, the half's maximum].
+    const float hmax = whole ? top.score : fold_waves(fold_s, fold_i, gslot * kSlotWaves, kSlotWaves).score;
+    const int lxb = int(__float_as_uint(lx) >> 16);
+    const int span = (on & (lx > 0.0f) & (hmax >= lx)) ? int(__float_as_uint(hmax) >> 16) - lxb + 1 : 0;
+    const bool tab = span > 0 && span <= kXFloors;
+    uint32_t* gxf = xfloors + (whole ? 0 : gslot) * kXFloors;
+    if (gumbel && tab) {
+        // one table per Gumbel half; a whole row's slots share slot 0's
+        if (!whole || slot == 0)
+            for (int j = st; j < span; j += kSlotThreads) gxf[j] = hash_floor(p, nvr::bf16_to_f32(uint16_t(lxb + j)));
+    }
+
+    // Phase 3: window 0 of each Gumbel wave's compaction.
+    uint32_t* queue = lds + wave * kQ;
+    const uint32_t lane_code = uint32_t(lane) << 3;
+    int n = 0;
+    if (gumbel) n = compact_window_dense<C>(w, lx, queue, 0, kCap, lane_code);
+    if (lane == 0) counts[wave] = n;
+    __syncthreads();
+
+    // Phase 4: scoring. A Gumbel half whose every queue fits scores the front
+    // of each queue itself and leaves the back to its helper; otherwise each
+    // wave works through its own windows.
+    bool fits = true;
+#pragma unroll
+    for (int i = 0; i < kSlotWaves; ++i) fits &= counts[gslot * kSlotWaves + i] <= kCap;
+    Best best = gumbel ? seeded : Best{-__builtin_inff(), nvr::kNoIndex};
+    if (gumbel) {
+        const int base = slot * kSlotThreads + sw * kWave;
+        if (fits) {
+            const int end = whole ? n : helper_split(n);
+            if (tab) score_queue<true>(queue, 0, end, lane, base, stride, p, gxf, lxb, best);
+            else score_queue<false>(queue, 0, end, lane, base, stride, p, gxf, lxb, best);
+        } else if (n > 2 * kCap) {
+            score_in_place(row, first, stride, chunks, lx, p, best);
+        } else {
+            for (int window = 0;; window += kCap) {
+                const int m = window == 0 ? n : compact_window_dense<C>(w, lx, queue, window, kCap, lane_code);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (tab) score_queue<true>(queue, 0, min(m, kCap), lane, base, stride, p, gxf, lxb, best);
+                else score_queue<false>(queue, 0, min(m, kCap), lane, base, stride, p, gxf, lxb, best);
+                if (m <= kCap) break;
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+        }
+    } else if (helps && fits) {
+        const int gw = gslot * kSlotWaves + sw;
+        const int gn = counts[gw];
+        const int base = gslot * kSlotThreads + sw * kWave;
+        if (tab) score_queue<true>(lds + gw * kQ, helper_split(gn), gn, lane, base, stride, p, gxf, lxb, best);
+        else score_queue<false>(lds + gw * kQ, helper_split(gn), gn, lane, base, stride, p, gxf, lxb, best);
+    }
+
+    // Phase 5: the Gumbel row's best over every wave that scored for it.
+    best = wave_argmax(best);
+    if (lane == 0) { fold_s[2 * kPairWaves + wave] = best.score; fold_i[2 * kPairWaves + wave] = best.index; }
+    __syncthreads();
+    if (tid == 0 || tid == kSlotThreads) {
+        const int gs = tid / kSlotThreads;  // this thread's slot
+        const bool g = temps[gs == 0 ? b : r1] > 0.0f;
+        if (g && (!whole || gs == 0)) {
+            const Best fin = fold_waves(fold_s + 2 * kPairWaves, fold_i + 2 * kPairWaves, 0, kPairWaves);
+            if (whole) out[b] = fin.index == nvr::kNoIndex ? 0 : fin.index;
+            else deposit(state, gs == 0 ? b : r1, fin, out, partner_key);
+        }
+    }
 }
 
 // Generic partitions (unaligned rows or vocab % 8 != 0): 2048-token
@@ -727,6 +1108,20 @@ int launch_resident(nv_context* c, const uint16_t* logits, const float* temps, c
     return nvr::launch_status();
 }
 
+int launch_paired(nv_context* c, const uint16_t* logits, const float* temps, const uint64_t* seeds, int* out,
+                  int batch, int vocab, int chunks_per_lane) {
+    const dim3 grid = dim3(unsigned(batch)), block = dim3(unsigned(kPairThreads));
+    auto* state = static_cast<uint64_t*>(c->pair_state);
+    switch (chunks_per_lane) {
+    case 4: hipLaunchKernelGGL(sample_paired<4>, grid, block, kPairLdsBytes, c->stream, logits, temps, seeds, out, state, vocab, batch); break;
+    case 8: hipLaunchKernelGGL(sample_paired<8>, grid, block, kPairLdsBytes, c->stream, logits, temps, seeds, out, state, vocab, batch); break;
+    case 12: hipLaunchKernelGGL(sample_paired<12>, grid, block, kPairLdsBytes, c->stream, logits, temps, seeds, out, state, vocab, batch); break;
+    case 16: hipLaunchKernelGGL(sample_paired<16>, grid, block, kPairLdsBytes, c->stream, logits, temps, seeds, out, state, vocab, batch); break;
+    default: hipLaunchKernelGGL(sample_paired<20>, grid, block, kPairLdsBytes, c->stream, logits, temps, seeds, out, state, vocab, batch); break;
+    }
+    return nvr::launch_status();
+}
+
 int launch_parallel(nv_context* c, const void* logits, const void* temps, const void* seeds, void* out,
                     void* partial_scores, void* partial_ids, int batch, int vocab) {
     const int64_t ref_parts = (int64_t(vocab) + kRefPartition - 1) / kRefPartition;
@@ -743,9 +1138,12 @@ int launch_parallel(nv_context* c, const void* logits, const void* temps, const 
     // mixed and T = 1 batches).
     const int min_rows = c->cu_count > 0 ? c->cu_count : 256;
     const int64_t lane_chunks = (int64_t(vocab) / 8 + 1023) / 1024;  // per lane of the row's 1024 threads
-    if (batch >= min_rows && vector_rows(logits, vocab) && lane_chunks <= kResMaxChunks)
+    if (batch >= min_rows && vector_rows(logits, vocab) && lane_chunks <= kResMaxChunks) {
+        if (batch <= kPairRows && c->pair_state)
+            return launch_paired(c, l16, t, s, static_cast<int*>(out), batch, vocab, int((lane_chunks + 3) / 4 * 4));
         return launch_resident<kResThreads>(c, l16, t, s, static_cast<int*>(out), ps, pi, batch, vocab,
                                             int((lane_chunks + 3) / 4 * 4));
+    }
     int parts;
     if (vector_rows(logits, vocab) && batch <= kFullScoreRows) {
         parts = int(ref_parts);  // 2048-token partitions: the most blocks the scratch allows
@@ -788,6 +1186,15 @@ int bind_static_partials(nv_context* c) {
     void* ptr = nullptr;
     NVR_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
     c->static_partials = ptr;
+    return 0;
+}
+
+int create_pair_state(nv_context* c) {
+    void* ptr = nullptr;
+    const size_t bytes = sizeof(uint64_t) * 2 * size_t(kPairRows);
+    NVR_HIP(hipMalloc(&ptr, bytes));
+    c->pair_state = ptr;
+    NVR_HIP(hipMemset(ptr, 0, bytes));
     return 0;
 }
 

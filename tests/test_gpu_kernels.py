@@ -488,6 +488,43 @@ def test_sampling_mixed_batches_one_row_per_cu(gpu, greedy_rows):
         assert_bits_equal(out.download(np.int32, batch), want)
 
 
+@pytest.mark.parametrize("extra", [1, 37, 300])
+def test_sampling_more_rows_than_cus(gpu, extra):
+    """More rows than CUs: blocks of a greedy/Gumbel pair need not be resident
+    together, so a Gumbel half may prune against its own best lane score
+    after a bounded wait for its partner's; every row still matches the
+    oracle. Greedy and Gumbel rows interleave, with edge rows among them."""
+    batch, vocab = gpu.sm_count() + extra, 40000
+    logits, temps, seeds = _edge_rows(batch, vocab, 420 + extra)
+    temps[19:] = np.where(np.arange(19, batch) % 3 == 0, 0.0, np.float32(0.6))
+    want = ora.sample(logits, temps, seeds, batch, vocab, threads=8)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab), want)
+
+
+def test_sampling_paired_graph_replays(gpu):
+    """The one-row-per-CU sampler in a HIP graph: three replays with eager
+    calls on other inputs between them, each against the oracle (the rows'
+    exchange words must be left zero by every launch)."""
+    batch, vocab = gpu.sm_count(), 151936
+    logits, temps, seeds = sampling_batch(batch, vocab, seed=430)
+    other, otemps, oseeds = sampling_batch(batch, vocab, seed=431)
+    otemps = otemps[::-1].copy()  # Gumbel rows first
+    want = ora.sample(logits, temps, seeds, batch, vocab, threads=8)
+    owant = ora.sample(other, otemps, oseeds, batch, vocab, threads=8)
+    lb, tb, sb = up(gpu, logits), up(gpu, temps), up(gpu, seeds)
+    olb, otb, osb = up(gpu, other), up(gpu, otemps), up(gpu, oseeds)
+    parts = -(-vocab // 2048)
+    ps, pi = gpu.alloc(batch * parts * 4), gpu.alloc(batch * parts * 4)
+    out, oout = gpu.alloc(batch * 4), gpu.alloc(batch * 4)
+    graph = gpu.capture(lambda: gpu.sample_parallel(lb, tb, sb, out, ps, pi, batch, vocab))
+    for _ in range(3):
+        gpu.sample_parallel(olb, otb, osb, oout, ps, pi, batch, vocab)
+        assert_bits_equal(oout.download(np.int32, batch), owant)
+        graph.replay()
+        gpu.sync()
+        assert_bits_equal(out.download(np.int32, batch), want)
+
+
 def test_sampling_reference_golden_vectors(gpu):
     """All 20 last-position logit rows of the reference's validation run and
     the tokens its GPU greedy sampler picked (row 4: an exact tie, lower index
