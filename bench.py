@@ -497,14 +497,14 @@ COPY_CASE, COPY_BYTES = "copy_256mb", 256 << 20
 CASE_KERNEL = {
     COPY_CASE: "__amd_rocclr_copyBuffer",
     "silu_8192x6144": "silu16",
-    "add_rms_8192x1024": "rms_rows_fast<4, true>",
+    "add_rms_8192x1024": "rms_rows_fast<4, true, false>",
     "qkv_rope_8192": "qkv_rope_d128<true, 4>",
     "embedding_16384": "gather_rows16",
     "kv_write_16384": "kv_write16",
     "attention_decode_64x4096": "attention_ordered<128, 2, 2, false, false>",
-    "sampling_256x151936": "sample_resident<",
-    "sampling_greedy": "sample_resident<",
-    "sampling_gumbel": "sample_resident<",
+    "sampling_256x151936": "sample_paired<",
+    "sampling_greedy": "sample_paired<",
+    "sampling_gumbel": "sample_paired<",
 }
 TRAFFIC_CASES = [COPY_CASE, "silu_8192x6144", "add_rms_8192x1024", "qkv_rope_8192", "embedding_16384",
                  "kv_write_16384", "attention_decode_64x4096", "sampling_gumbel"]
@@ -799,6 +799,13 @@ def assign_dispatches(order, disp) -> tuple[dict, str]:
     return result, "ok"
 
 
+def under_profiler(env=None) -> bool:
+    """True when this process runs under rocprofv3 (its tool library is
+    preloaded, or its ROCPROF_* settings are in the environment)."""
+    env = os.environ if env is None else env
+    return "rocprofiler" in env.get("LD_PRELOAD", "") or any(k.startswith("ROCPROF") for k in env)
+
+
 def kernel_times(rounds, only, timeout_s=420) -> tuple[dict, str]:
     """{case: (kernel name, median kernel us, timed dispatches)} from a child
     run of this script under rocprofv3 --kernel-trace, and a status note.
@@ -809,6 +816,11 @@ def kernel_times(rounds, only, timeout_s=420) -> tuple[dict, str]:
     import shutil
     import tempfile
 
+    if under_profiler():
+        # The tracer's launcher replaces itself with its target program; under
+        # an outer profiler's preloaded library that process has already
+        # initialised the GPU, and such an exec must not happen.
+        return {}, "not run (this process runs under a profiler)"
     prof = shutil.which("rocprofv3") or ("/opt/rocm/bin/rocprofv3" if os.path.exists("/opt/rocm/bin/rocprofv3")
                                          else None)
     if prof is None:

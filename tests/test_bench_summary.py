@@ -72,7 +72,7 @@ def test_traffic_table_counts_request_sizes_and_applies_the_copy_calibration(tmp
 
 
 def test_valu_table_splits_the_sampling_cases_in_launch_order(tmp_path):
-    name = "void (anonymous namespace)::sample_resident<20, 1024>(...)"
+    name = "void (anonymous namespace)::sample_paired<20>(...)"
     ds = []
     for valu in (100, 200, 300):  # mixed, greedy, Gumbel: two dispatches each
         for _ in range(2):
@@ -149,3 +149,9 @@ def test_sweep_slot_layouts_are_distinct_slots_inside_the_cache():
             assert slots.min() >= 0 and slots.max() < blocks * bench.BS
             # whole 256-token blocks stay together (slot % 256 == token % 256)
             assert np.array_equal(slots % bench.BS, np.arange(tokens) % bench.BS)
+
+
+def test_kernel_trace_child_is_not_started_under_a_profiler():
+    assert bench.under_profiler({"LD_PRELOAD": "/opt/rocm/lib/librocprofiler-sdk-tool.so"})
+    assert bench.under_profiler({"ROCPROF_COUNTERS": "pmc: SQ_WAVES"})
+    assert not bench.under_profiler({"LD_PRELOAD": "", "PATH": "/usr/bin"})
