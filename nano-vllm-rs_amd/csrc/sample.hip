@@ -791,7 +791,10 @@ __device__ __forceinline__ DealTemps load_deal(const float* temps, int batch, in
     return d;
 }
 __device__ __forceinline__ int partner_row(const float* temps, const DealTemps& d, int batch, int b, int lane) {
-    const bool gum = d.own > 0.0f;
+    // Every value below is wave-uniform; taking the row's own temperature
+    // from the first lane lets the compiler keep the rank and both walks in
+    // scalar registers instead of running them as per-lane divergent loops.
+    const bool gum = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(d.own))) > 0.0f;
     const bool one_round = batch <= kWave * kDealLoads;
     uint64_t kinds[kDealLoads];  // bit l of kinds[c]: row 64 c + l is Gumbel
 #pragma unroll
@@ -819,11 +822,14 @@ __device__ __forceinline__ int partner_row(const float* temps, const DealTemps& 
     int seen = 0;
     for (int c = 0; c < nc; ++c) {
         const uint64_t valid = c * kWave + kWave <= batch ? ~uint64_t(0) : (uint64_t(1) << (batch - c * kWave)) - 1;
-        uint64_t m = (gum ? ~kind_mask(c) : kind_mask(c)) & valid;  // rows of the other kind
+        const uint64_t m = (gum ? ~kind_mask(c) : kind_mask(c)) & valid;  // rows of the other kind
         const int n = __popcll(m);
         if (rank < seen + n) {
-            for (int k = rank - seen; k > 0; --k) m &= m - 1;
-            return c * kWave + __builtin_ctzll(m);
+            // The (rank - seen)-th set bit of m: the one lane whose bit is set
+            // and which counts exactly that many set bits of m below itself.
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u));
+            const uint64_t at = __ballot(((m >> lane) & 1) != 0 && int(below) == rank - seen);
+            return c * kWave + __builtin_ctzll(at);
         }
         seen += n;
     }
