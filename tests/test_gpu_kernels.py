@@ -501,6 +501,18 @@ def test_sampling_more_rows_than_cus(gpu, extra):
     assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab), want)
 
 
+def test_sampling_beyond_paired_rows(gpu):
+    """Past the context's 16384 rows of exchange words the whole-row
+    resident kernel samples every row (one block per row, no partner):
+    16424 rows of 8200 tokens, edge rows first, greedy and Gumbel rows
+    interleaved, against the oracle."""
+    batch, vocab = 16384 + 40, 8200
+    logits, temps, seeds = _edge_rows(batch, vocab, 440)
+    temps[19:] = np.where(np.arange(19, batch) % 3 == 0, 0.0, np.float32(0.6))
+    want = ora.sample(logits, temps, seeds, batch, vocab, threads=8)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab), want)
+
+
 def test_sampling_paired_graph_replays(gpu):
     """The one-row-per-CU sampler in a HIP graph: three replays with eager
     calls on other inputs between them, each against the oracle (the rows'
