@@ -557,10 +557,16 @@ __device__ __forceinline__ int compact_window(uint4 (&w)[C], float lx, uint32_t*
 // `capacity` entries followed by one spare per lane; a non-candidate stores
 // into its lane's spare, a candidate past the window into min(position,
 // capacity + lane), a spare too (each of those slots holds junk).
+typedef __attribute__((address_space(3))) uint32_t lds_word;
 template <int C>
 __device__ __forceinline__ int compact_window_dense(uint4 (&w)[C], float lx, uint32_t* queue, int window,
                                                     int capacity, uint32_t lane_code) {
     const uint32_t spare = uint32_t(capacity) + (lane_code >> 3);
+    // LDS byte addresses: the queue's (wave-uniform, so scalar) and this
+    // lane's spare entry.
+    const uint32_t qbase =
+        __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<size_t>((lds_word*)queue)));
+    const uint32_t spare_at = qbase + 4 * spare;
     int n = -window;
 #pragma unroll
     for (int k = 0; k < C; ++k) {
@@ -573,16 +579,35 @@ __device__ __forceinline__ int compact_window_dense(uint4 (&w)[C], float lx, uin
             xb[i] = (i & 1) ? (words[i / 2] & 0xffff0000u) : (words[i / 2] << 16);
             bal[i] = __ballot(__uint_as_float(xb[i]) >= lx);
         }
+        if (n >= 0 && n + 8 * kWave <= capacity) {
+            // Every position of this chunk lies in [0, capacity): a candidate's
+            // address is qn (the queue's address of entry n, scalar) plus 4
+            // times the candidates below it.
+            const uint32_t code = lane_code | uint32_t(k << 9);
+            uint32_t qn = qbase + 4 * uint32_t(n);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t pos = __builtin_amdgcn_mbcnt_hi(uint32_t(bal[i] >> 32),
-                                                           __builtin_amdgcn_mbcnt_lo(uint32_t(bal[i]), uint32_t(n)));
-            // the ballot is the candidate lanes' mask: select on it directly
-            // (as a plain select the compiler masks exec around the position)
-            uint32_t to;
-            __asm__("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(to) : "v"(spare), "v"(min(pos, spare)), "s"(bal[i]));
-            queue[to] = xb[i] | lane_code | uint32_t(k << 9 | i);
-            n += int(__popcll(bal[i]));
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t below = __builtin_amdgcn_mbcnt_hi(uint32_t(bal[i] >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo(uint32_t(bal[i]), 0u));
+                __asm__("" : "+s"(qn));  // kept whole: one shift-add per lane
+                uint32_t to;
+                __asm__("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(to) : "v"(spare_at), "v"(qn + 4 * below), "s"(bal[i]));
+                *reinterpret_cast<lds_word*>(size_t(to)) = xb[i] | code | uint32_t(i);
+                qn += 4 * uint32_t(__popcll(bal[i]));
+            }
+            n = int((qn - qbase) / 4);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
+                    uint32_t(bal[i] >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(bal[i]), uint32_t(n)));
+                // the ballot is the candidate lanes' mask: select on it directly
+                // (as a plain select the compiler masks exec around the position)
+                uint32_t to;
+                __asm__("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(to) : "v"(spare), "v"(min(pos, spare)), "s"(bal[i]));
+                queue[to] = xb[i] | lane_code | uint32_t(k << 9 | i);
+                n += int(__popcll(bal[i]));
+            }
         }
     }
     return n;
