@@ -488,6 +488,22 @@ def test_sampling_mixed_batches_one_row_per_cu(gpu, greedy_rows):
         assert_bits_equal(out.download(np.int32, batch), want)
 
 
+def test_sampling_one_row_per_cu_queue_windows(gpu):
+    """One row per CU at temperatures whose candidates overflow a wave's LDS
+    queue (2240 entries) without reaching twice that. A numpy model of these
+    N(0, 3) rows puts 76-83% of the waves at T = 0.8-0.9 in that range. Those
+    waves compact and score in windows; the compaction's clamped positions
+    then feed the scored queue. Greedy rows, T = 0.6 rows (queues that fit) and
+    T = 1.0 rows (scored in place) are mixed in, so every path of the
+    paired kernel runs in one launch, against the oracle."""
+    batch, vocab = gpu.sm_count(), 151936
+    logits = ora.normal_bf16((batch, vocab), 460, 0.0, 3.0)
+    temps = np.array([(0.0, 0.8, 0.85, 0.9, 0.6, 1.0, 0.75)[r % 7] for r in range(batch)], np.float32)
+    seeds = np.array([ora.sampling_seed(461, r, 3) for r in range(batch)], np.uint64)
+    want = ora.sample(logits, temps, seeds, batch, vocab, threads=8)
+    assert_bits_equal(_run_sampler(gpu, logits, temps, seeds, batch, vocab), want)
+
+
 @pytest.mark.parametrize("extra", [1, 37, 300])
 def test_sampling_more_rows_than_cus(gpu, extra):
     """More rows than CUs: blocks of a greedy/Gumbel pair need not be resident
