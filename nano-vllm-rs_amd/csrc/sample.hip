@@ -885,13 +885,10 @@ __device__ __forceinline__ float exchange_s0(uint64_t* state, int r, int half, f
 
 // Y exchange (one thread): meet the other half's result; the second half to
 // arrive writes the token and leaves both words zero for the next launch.
-// `seen` is a value of Y read earlier by this half: when it already holds
-// the other half's key, this half is the second without another atomic.
-__device__ __forceinline__ void deposit(uint64_t* state, int r, const Best& b, int* out, uint64_t seen = 0) {
+__device__ __forceinline__ void deposit(uint64_t* state, int r, const Best& b, int* out) {
     uint64_t* x = state + 2 * int64_t(r);
     const uint64_t key = result_key(b);
-    const uint64_t old =
-        seen != 0 ? seen : __hip_atomic_fetch_max(x + 1, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t old = __hip_atomic_fetch_max(x + 1, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (old == 0) return;
     const uint64_t m = old > key ? old : key;
     out[r] = (m >> 32) == 1 ? 0 : int(0x7fffffff - uint32_t(m));
@@ -965,26 +962,21 @@ __global__ __launch_bounds__(kPairThreads) void sample_paired(const uint16_t* __
     const bool whole = r1 == b;  // both halves of row b in this block
     const Best top = whole ? fold_waves(fold_s, fold_i, 0, kPairWaves)
                            : fold_waves(fold_s, fold_i, slot * kSlotWaves, kSlotWaves);
-    if (!gumbel) {
-        if (whole) {  // a whole greedy row: done (every wave of the block leaves here)
-            if (tid == 0) out[r] = top.index == nvr::kNoIndex ? 0 : top.index;
-            return;
-        }
-        if (st == 0) deposit(state, r, top, out);
+    if (!gumbel && whole) {  // a whole greedy row: done (every wave of the block leaves here)
+        if (tid == 0) out[r] = top.index == nvr::kNoIndex ? 0 : top.index;
+        return;
     }
 
     // s0 of the half (or of the row); a split Gumbel row trades its halves'.
     const Best seeded = whole ? fold_waves(fold_s + kPairWaves, fold_i + kPairWaves, 0, kPairWaves)
                               : fold_waves(fold_s + kPairWaves, fold_i + kPairWaves, slot * kSlotWaves, kSlotWaves);
-    // A split Gumbel half reads Y once its s0 is settled: its greedy partner
-    // has usually deposited by then, and the read's round trip overlaps the
-    // compaction instead of ending the launch.
-    uint64_t partner_key = 0;
-    if (gumbel && !whole && st == 0) {
-        slot_s0[slot] = exchange_s0(state, r, slot, seeded.score);
-        partner_key = __hip_atomic_load(state + 2 * int64_t(r) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (gumbel && !whole && st == 0) slot_s0[slot] = exchange_s0(state, r, slot, seeded.score);
     __syncthreads();
+    // A greedy half deposits its maximum here, while the Gumbel half compacts.
+    // Before the barrier its round trip would hold that compaction back, and
+    // so would any vector load in flight there: the memory counter retires in
+    // issue order, so the next wait for one waits for all of them.
+    if (!gumbel && !whole && st == 0) deposit(state, r, top, out);
 
     // The Gumbel half whose queues this wave compacts or helps score: its own
     // slot, or (a greedy half split from a Gumbel row's) the other slot.
@@ -1065,7 +1057,7 @@ __global__ __launch_bounds__(kPairThreads) void sample_paired(const uint16_t* __
         if (g && (!whole || gs == 0)) {
             const Best fin = fold_waves(fold_s + 2 * kPairWaves, fold_i + 2 * kPairWaves, 0, kPairWaves);
             if (whole) out[b] = fin.index == nvr::kNoIndex ? 0 : fin.index;
-            else deposit(state, gs == 0 ? b : r1, fin, out, partner_key);
+            else deposit(state, gs == 0 ? b : r1, fin, out);
         }
     }
 }
