@@ -583,17 +583,21 @@ __device__ __forceinline__ int compact_window_dense(uint4 (&w)[C], float lx, uin
             // Every position of this chunk lies in [0, capacity): a candidate's
             // address is qn (the queue's address of entry n, scalar) plus 4
             // times the candidates below it.
-            const uint32_t code = lane_code | uint32_t(k << 9);
+            // The round's code in a register of its own, so that each entry is
+            // one or3 with the element index as an inline constant (no scalar
+            // move per element).
+            uint32_t code = lane_code | uint32_t(k << 9);
+            __asm__("" : "+v"(code));
             uint32_t qn = qbase + 4 * uint32_t(n);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const uint32_t below = __builtin_amdgcn_mbcnt_hi(uint32_t(bal[i] >> 32),
                                                                  __builtin_amdgcn_mbcnt_lo(uint32_t(bal[i]), 0u));
-                __asm__("" : "+s"(qn));  // kept whole: one shift-add per lane
                 uint32_t to;
                 __asm__("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(to) : "v"(spare_at), "v"(qn + 4 * below), "s"(bal[i]));
                 *reinterpret_cast<lds_word*>(size_t(to)) = xb[i] | code | uint32_t(i);
-                qn += 4 * uint32_t(__popcll(bal[i]));
+                // qn += 4 * popcount, one scalar shift-add
+                __asm__("s_lshl2_add_u32 %0, %1, %0" : "+s"(qn) : "s"(uint32_t(__popcll(bal[i]))) : "scc");
             }
             n = int((qn - qbase) / 4);
         } else {
@@ -1052,12 +1056,13 @@ __global__ __launch_bounds__(kPairThreads) void sample_paired(const uint16_t* __
     if (lane == 0) { fold_s[2 * kPairWaves + wave] = best.score; fold_i[2 * kPairWaves + wave] = best.index; }
     __syncthreads();
     if (tid == 0 || tid == kSlotThreads) {
-        const int gs = tid / kSlotThreads;  // this thread's slot
-        const bool g = temps[gs == 0 ? b : r1] > 0.0f;
-        if (g && (!whole || gs == 0)) {
+        // The first thread of each slot: its slot's row is r (b, or r1) and
+        // `gumbel` its kind, both known since the start (no load here, on the
+        // launch's last step).
+        if (gumbel && (!whole || slot == 0)) {
             const Best fin = fold_waves(fold_s + 2 * kPairWaves, fold_i + 2 * kPairWaves, 0, kPairWaves);
             if (whole) out[b] = fin.index == nvr::kNoIndex ? 0 : fin.index;
-            else deposit(state, gs == 0 ? b : r1, fin, out);
+            else deposit(state, r, fin, out);
         }
     }
 }
