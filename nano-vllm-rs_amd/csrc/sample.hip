@@ -505,17 +505,35 @@ __device__ __forceinline__ Best lane_best(uint4 (&w)[C], int stride, int first, 
 // The candidates of a Gumbel row pruned against s0 are exactly the logits
 // x >= lx, lx the smallest bf16 value with x * (1/T) >= (s0 - kNoiseMax) -
 // (|s0| + 34) * 2^-17 (x * (1/T) is nondecreasing in x; the margin covers
-// 1/T's and the score's roundings): a binary search over the order-preserving
-// 16-bit keys of the bf16 values (-inf .. +inf). -inf when pruning is off.
-__device__ __forceinline__ float candidate_floor(float s0, float inv_t, bool on) {
+// 1/T's and the score's roundings), in the order-preserving 16-bit keys of
+// the bf16 values (-inf .. +inf). bound * T lies within a few fp32 ulps of
+// that threshold, so its key (rounded toward -inf) is at most a step from
+// lx's: two steps up while the predicate fails, two down while the key below
+// passes, and the key is exact once it passes and the one below does not
+// (tests/cpp/candidate_floor_check.cpp compares it with the full search on
+// millions of (s0, T) pairs, edge cases included). Past the range
+// where that holds, or if the steps do not settle, a binary search over all
+// keys (16 dependent steps) decides. -inf when pruning is off.
+__device__ __forceinline__ float candidate_floor(float s0, float inv_t, float t, bool on) {
     if (!on) return -__builtin_inff();
     const float bound = (s0 - kNoiseMax) - (__builtin_fabsf(s0) + 34.0f) * 0x1.0p-17f;
     auto value = [](int key) { return nvr::bf16_to_f32(uint16_t(key >= 0x8000 ? key - 0x8000 : 0xffff - key)); };
+    auto pass = [&](int key) { return value(key) * inv_t >= bound; };
+    const float v0 = bound * t;
+    const uint32_t u = __float_as_uint(v0);
+    int key = (u & 0x80000000u) ? 0xffff - int((u >> 16) + ((u & 0xffffu) != 0u)) : int(u >> 16) + 0x8000;
+    if (__builtin_fabsf(v0) >= 0x1.0p-100f && __builtin_fabsf(v0) <= 0x1.0p+100f) {
+        key += !pass(key);
+        key += !pass(key);
+        key -= pass(key - 1);
+        key -= pass(key - 1);
+        if (pass(key) && !pass(key - 1)) return value(key);
+    }
     int lo = 0x007f, hi = 0xff80;  // -inf, +inf; +inf always qualifies
-    if (value(lo) * inv_t >= bound) hi = lo;
+    if (pass(lo)) hi = lo;
     while (hi - lo > 1) {
         const int mid = (lo + hi) >> 1;
-        if (value(mid) * inv_t >= bound) hi = mid;
+        if (pass(mid)) hi = mid;
         else lo = mid;
     }
     return value(hi);
@@ -707,7 +725,7 @@ __global__ __launch_bounds__(TPB) void sample_resident(const uint16_t* __restric
     const Best seeded = block_fold<kW>(own, fold_s + kW, fold_i + kW);
     const float s0 = seeded.score, inv_t = 1.0f / temperature;
     const bool on = __builtin_fabsf(s0) < __builtin_inff() && inv_t < __builtin_inff();
-    const float lx = candidate_floor(s0, inv_t, on);
+    const float lx = candidate_floor(s0, inv_t, temperature, on);
 
     // Phase 3: each wave compacts its candidates into its LDS queue (ballot +
     // mbcnt) and scores them, in rounds of kQ entries when there are
@@ -992,7 +1010,7 @@ __global__ __launch_bounds__(kPairThreads) void sample_paired(const uint16_t* __
     const float s0 = whole ? seeded.score : slot_s0[gslot];
     const float inv_t = 1.0f / gt;
     const bool on = __builtin_fabsf(s0) < __builtin_inff() && inv_t < __builtin_inff();
-    const float lx = candidate_floor(s0, inv_t, on);
+    const float lx = candidate_floor(s0, inv_t, gt, on);
     const Pruner p{s0, inv_t, gt, gseed, on, floors};
     // Tabulated hash floors over the candidate values [lx, the half's maximum].
     const float hmax = whole ? top.score : fold_waves(fold_s, fold_i, gslot * kSlotWaves, kSlotWaves).score;

@@ -7,7 +7,9 @@
   config checks on the CPU; on a GPU the batch contract, the fused-attention
   choice, the forward against the CPU oracle stage by stage, fused against
   split attention, graph replay against the eager forward and decode against
-  prefill."""
+  prefill;
+- tests/cpp/candidate_floor_check: the sampler's direct candidate floor
+  against the binary search it replaces (host only)."""
 import os
 import subprocess
 
@@ -28,6 +30,13 @@ def _run(binary: str, suite: str) -> str:
 def test_cpp_host_argument_checks():
     out = _run("test_gpu_host", "cpu")
     assert "FAILED" not in out and " passed" in out
+
+
+def test_candidate_floor_direct_form_equals_search():
+    """sample.hip's candidate floor from bound * T and a few predicate steps
+    gives the same bits as the binary search over every bf16 key."""
+    out = _run("candidate_floor_check", "2000000")
+    assert " 0 mismatches" in out, out
 
 
 def test_cpp_model_metadata_and_config():
