@@ -883,10 +883,17 @@ __device__ __forceinline__ int partner_row(const float* temps, const DealTemps& 
     return b;
 }
 
-// Best over waves [w0, w0 + n) of a fold array.
+// Best over waves [w0, w0 + n) of a fold array (n <= 16), in every lane (all
+// lanes active): lane l of each 16-lane row takes entry l, then a butterfly
+// inside the row (DPP moves). `better` orders (score, index) pairs totally
+// and no NaN score reaches a fold, so the winner is the one a left-to-right
+// fold finds, in 4 dependent steps instead of n - 1.
 __device__ __forceinline__ Best fold_waves(const float* s, const int* i, int w0, int n) {
-    Best r{s[w0], i[w0]};
-    for (int w = 1; w < n; ++w) consider(r, s[w0 + w], i[w0 + w]);
+    const int l = int(threadIdx.x) & 15;
+    Best r{-__builtin_inff(), nvr::kNoIndex};
+    if (l < n) r = Best{s[w0 + l], i[w0 + l]};
+#pragma unroll
+    for (int mask = 8; mask > 0; mask >>= 1) consider(r, nvr::xor_lane(r.score, mask), nvr::xor_lane(r.index, mask));
     return r;
 }
 
@@ -993,7 +1000,7 @@ __global__ __launch_bounds__(kPairThreads) void sample_paired(const uint16_t* __
     const Best seeded = whole ? fold_waves(fold_s + kPairWaves, fold_i + kPairWaves, 0, kPairWaves)
                               : fold_waves(fold_s + kPairWaves, fold_i + kPairWaves, slot * kSlotWaves, kSlotWaves);
     if (gumbel && !whole && st == 0) slot_s0[slot] = exchange_s0(state, r, slot, seeded.score);
-    __syncthreads();
+    if (!whole) __syncthreads();  // a whole row exchanges nothing here
     // A greedy half deposits its maximum here, while the Gumbel half compacts.
     // Before the barrier its round trip would hold that compaction back, and
     // so would any vector load in flight there: the memory counter retires in
@@ -1073,12 +1080,12 @@ __global__ __launch_bounds__(kPairThreads) void sample_paired(const uint16_t* __
     best = wave_argmax(best);
     if (lane == 0) { fold_s[2 * kPairWaves + wave] = best.score; fold_i[2 * kPairWaves + wave] = best.index; }
     __syncthreads();
-    if (tid == 0 || tid == kSlotThreads) {
-        // The first thread of each slot: its slot's row is r (b, or r1) and
-        // `gumbel` its kind, both known since the start (no load here, on the
-        // launch's last step).
-        if (gumbel && (!whole || slot == 0)) {
-            const Best fin = fold_waves(fold_s + 2 * kPairWaves, fold_i + 2 * kPairWaves, 0, kPairWaves);
+    if (sw == 0 && gumbel && (!whole || slot == 0)) {
+        // The first wave of each Gumbel slot: its slot's row is r (b, or r1)
+        // and `gumbel` its kind, both known since the start (no load here, on
+        // the launch's last step).
+        const Best fin = fold_waves(fold_s + 2 * kPairWaves, fold_i + 2 * kPairWaves, 0, kPairWaves);
+        if (st == 0) {
             if (whole) out[b] = fin.index == nvr::kNoIndex ? 0 : fin.index;
             else deposit(state, r, fin, out);
         }
