@@ -611,9 +611,18 @@ __device__ __forceinline__ int compact_window_dense(uint4 (&w)[C], float lx, uin
             for (int i = 0; i < 8; ++i) {
                 const uint32_t below = __builtin_amdgcn_mbcnt_hi(uint32_t(bal[i] >> 32),
                                                                  __builtin_amdgcn_mbcnt_lo(uint32_t(bal[i]), 0u));
-                uint32_t to;
-                __asm__("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(to) : "v"(spare_at), "v"(qn + 4 * below), "s"(bal[i]));
-                *reinterpret_cast<lds_word*>(size_t(to)) = xb[i] | code | uint32_t(i);
+                // Only the candidate lanes write: exec is the ballot for the one
+                // LDS store (restored at once), so no per-lane select. The
+                // compiler's LDS counter waits stay conservative (LDS
+                // operations of a wave complete in order).
+                uint64_t saved;
+                __asm__ volatile(
+                    "s_and_saveexec_b64 %0, %3\n\t"
+                    "ds_write_b32 %1, %2\n\t"
+                    "s_mov_b64 exec, %0"
+                    : "=&s"(saved)
+                    : "v"(qn + 4 * below), "v"(xb[i] | code | uint32_t(i)), "s"(bal[i])
+                    : "memory", "scc");
                 // qn += 4 * popcount, one scalar shift-add
                 __asm__("s_lshl2_add_u32 %0, %1, %0" : "+s"(qn) : "s"(uint32_t(__popcll(bal[i]))) : "scc");
             }
