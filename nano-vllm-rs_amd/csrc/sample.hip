@@ -570,8 +570,9 @@ __device__ __forceinline__ int compact_window(uint4 (&w)[C], float lx, uint32_t*
 
 // compact_window for waves that run two to a SIMD, with the same entries
 // in the same order: a chunk's eight ballots are taken before any position,
-// and every lane stores for every element, so no store needs an exec mask
-// and no element waits on the previous one's scalar count. The queue holds
+// so no element waits on the previous one's scalar count. Where a chunk's
+// every position lies inside the window, each element is one store under
+// exec = its ballot. Otherwise every lane stores: the queue holds
 // `capacity` entries followed by one spare per lane; a non-candidate stores
 // into its lane's spare, a candidate past the window into min(position,
 // capacity + lane), a spare too (each of those slots holds junk).
@@ -580,11 +581,9 @@ template <int C>
 __device__ __forceinline__ int compact_window_dense(uint4 (&w)[C], float lx, uint32_t* queue, int window,
                                                     int capacity, uint32_t lane_code) {
     const uint32_t spare = uint32_t(capacity) + (lane_code >> 3);
-    // LDS byte addresses: the queue's (wave-uniform, so scalar) and this
-    // lane's spare entry.
+    // The queue's LDS byte address (wave-uniform, so scalar).
     const uint32_t qbase =
         __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<size_t>((lds_word*)queue)));
-    const uint32_t spare_at = qbase + 4 * spare;
     int n = -window;
 #pragma unroll
     for (int k = 0; k < C; ++k) {
