@@ -27,10 +27,13 @@
 // 2048-token partitions scanned element by element, then stage 3.
 //
 // Large batches (at least one row per CU, rows of at most 20 * 8192 tokens)
-// take one launch instead: sample_resident gives each row a 1024-thread block
-// that keeps the whole row in registers (Qwen3's 151936 logits are 76 VGPRs a
-// lane), so the row is read from HBM once and never re-read, and no partials
-// or second launch are needed.
+// take one launch instead, in which a 1024-thread block keeps a row's worth
+// of logits in registers (Qwen3's 151936 logits are 76 VGPRs a lane), so every
+// logit is read from HBM once and no partials or second launch are needed.
+// sample_paired (up to 16384 rows, with the context's exchange words) gives
+// each block half of its own row and half of a partner row of the other kind,
+// a greedy row with a Gumbel row; sample_resident (otherwise) gives each block
+// one whole row.
 #include "../../include/nano_hip.h"
 #include "nvr_device.h"
 #include "nvr_internal.h"
