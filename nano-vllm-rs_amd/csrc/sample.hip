@@ -615,8 +615,10 @@ __device__ __forceinline__ int compact_window_dense(uint4 (&w)[C], float lx, uin
                                                                  __builtin_amdgcn_mbcnt_lo(uint32_t(bal[i]), 0u));
                 // Only the candidate lanes write: exec is the ballot for the one
                 // LDS store (restored at once), so no per-lane select. The
-                // compiler's LDS counter waits stay conservative (LDS
-                // operations of a wave complete in order).
+                // compiler's wait counting does not see this store. Reads by
+                // the same wave need no wait (a wave's LDS operations complete
+                // in order); a caller that hands the queue to other waves
+                // waits for it explicitly before the barrier.
                 uint64_t saved;
                 __asm__ volatile(
                     "s_and_saveexec_b64 %0, %3\n\t"
@@ -1047,6 +1049,9 @@ __global__ __launch_bounds__(kPairThreads) void sample_paired(const uint16_t* __
     const uint32_t lane_code = uint32_t(lane) << 3;
     int n = 0;
     if (gumbel) n = compact_window_dense<C>(w, lx, queue, 0, kCap, lane_code);
+    // The helper waves read this queue after the barrier: wait for the
+    // compaction's stores, which the compiler's own waits do not count.
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     if (lane == 0) counts[wave] = n;
     __syncthreads();
 
