@@ -365,6 +365,38 @@ def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=(), sw
                       [lambda j=j, T=T: gpu.embedding(toks[j], tables[j % 3], eouts[j], T, H, V) for j in range(6)],
                       bytes_embedding(T, H), T))
 
+    # Copy ceilings: plain 1:1 copies of 64 MiB and 128 MiB in all (half read,
+    # half written), each through the library's faster copy kernel at that
+    # size. 64 MiB: the row gather (nv_embedding) over identity ids, 16384
+    # rows of 2 KiB (the KV write's 16 rows per wave would fill half the CUs).
+    # 128 MiB: nv_kv_write of k, v [16384, 8, 128] through identity slots
+    # (every load of a wave in flight before its stores; 0.63 of peak for the
+    # gather at this size against 0.78). The streaming kernels'
+    # "copy_ceiling" compares them with the copy of about their own traffic.
+    if want("copy_64mb"):
+        rows = 16384
+        s = sets_for(2 * rows * H * 2)
+        srcs = [fill.normal(rows * H * 2) for _ in range(s)]
+        dsts = [gpu.alloc(rows * H * 2) for _ in range(s)]
+        ident = fill.ints(np.arange(rows, dtype=np.int32))
+        cases.append(("copy_64mb", f"copy: row gather of {rows} rows of 2 KiB over identity ids",
+                      [lambda i=i, rows=rows, ident=ident, srcs=srcs, dsts=dsts: gpu.embedding(ident, srcs[i], dsts[i], rows, H, rows)
+                       for i in range(s)],
+                      bytes_embedding(rows, H), rows))
+    if want("copy_128mb"):
+        rows = 16384
+        half = rows * KVH * D * 2
+        s = sets_for(4 * half)
+        cks = [fill.normal(half) for _ in range(s)]
+        cvs = [fill.normal(half) for _ in range(s)]
+        ckc = [gpu.alloc(half) for _ in range(s)]
+        cvc = [gpu.alloc(half) for _ in range(s)]
+        cid = fill.ints(np.arange(rows, dtype=np.int32))
+        cases.append(("copy_128mb", f"copy: KV write of k, v [{rows},8,128] through identity slots",
+                      [lambda i=i, rows=rows: gpu.kv_write(cks[i], cvs[i], cid, ckc[i], cvc[i], rows, KVH, D, BS,
+                                                           rows // BS) for i in range(s)],
+                      bytes_kv_write(rows), rows))
+
     # Paged KV write, k/v [16384, 8, 128] into the per-layer caches of a
     # 28-layer layout ([128, 256, 8, 128] per layer and per K/V, 3.5 GiB in
     # all); launch l writes layer l from source set l mod 5. Slots come from a
@@ -506,6 +538,9 @@ CASE_KERNEL = {
     "sampling_greedy": "sample_paired<",
     "sampling_gumbel": "sample_paired<",
 }
+# The copy case of about each streaming kernel's traffic (64 or 128 MiB).
+COPY_CEILING = {"add_rms_8192x1024": "copy_64mb", "embedding_16384": "copy_64mb", "qkv_rope_4096": "copy_64mb",
+                "qkv_rope_8192": "copy_128mb", "kv_write_16384": "copy_128mb", "silu_8192x6144": "copy_128mb"}
 TRAFFIC_CASES = [COPY_CASE, "silu_8192x6144", "add_rms_8192x1024", "qkv_rope_8192", "embedding_16384",
                  "kv_write_16384", "attention_decode_64x4096", "sampling_gumbel"]
 READ_COUNTERS = ["TCC_EA0_RDREQ_32B_sum", "TCC_EA0_RDREQ_64B_sum", "TCC_EA0_RDREQ_128B_sum"]
@@ -964,6 +999,15 @@ def main() -> int:
         for name, tag in (("qkv_rope_8192", "perm of 32 blocks, seed 8192"), ("kv_write_16384", "perm of 128 blocks, seed 7")):
             if name in kernels:
                 kernels[name]["slot_layout"] = tag
+        # Each streaming kernel's rate as a fraction of the copy of about its
+        # own traffic (kernel time where both were traced, else event time).
+        for name, cname in COPY_CEILING.items():
+            if name in kernels and cname in kernels:
+                k, c = kernels[name], kernels[cname]
+                key = "kernel_us" if "kernel_us" in k and "kernel_us" in c else "us"
+                gbs, cgbs = k["bytes"] / k[key] / 1e3, c["bytes"] / c[key] / 1e3
+                k["copy_ceiling"] = {"case": cname, "GB/s": round(cgbs, 1), "frac": round(gbs / cgbs, 4),
+                                     "time": key}
         fold_layouts(kernels)
 
     # Dominant kernel of the step: the largest share of the step's HBM bytes
