@@ -755,8 +755,11 @@ def cpu_baseline(tokens: int, layers: int, runs: int = 5) -> dict:
         step(layers)
         times.append(time.perf_counter() - t0)
     sec = float(np.median(times))
-    return {"value": T / sec, "unit": "tokens/s", "cores": threads, "hardware_concurrency": hw,
-            "affinity_cpus": affinity, "kind": "port",
+    # Algorithmic bytes of the step, counted as for the GPU chain.
+    nbytes = (bytes_embedding(T, H) + bytes_rms(T, H) + 2 * layers * bytes_add_rms(T, H)
+              + layers * bytes_qkv_rope(T, len(np.unique(pos))) + layers * bytes_silu(T, I))
+    return {"value": T / sec, "unit": "tokens/s", "GB/s": round(nbytes / sec / 1e9, 2), "cores": threads,
+            "hardware_concurrency": hw, "affinity_cpus": affinity, "kind": "port",
             "sample": f"oracle C restatement, full step ({layers} layers, T={T}, distinct per-layer inputs), "
                       f"{threads} threads, median of {len(times)} runs = {sec * 1e3:.1f} ms/step"}
 
