@@ -891,6 +891,18 @@ def kernel_times(rounds, only, timeout_s=420) -> tuple[dict, str]:
         shutil.rmtree(out, ignore_errors=True)
 
 
+def add_copy_ceilings(kernels):
+    """Each streaming kernel's rate as a fraction of the copy case of about its
+    own traffic (COPY_CEILING), by kernel time where both were traced, else by
+    event time; cases without their copy case get no field."""
+    for name, cname in COPY_CEILING.items():
+        if name in kernels and cname in kernels:
+            k, c = kernels[name], kernels[cname]
+            key = "kernel_us" if "kernel_us" in k and "kernel_us" in c else "us"
+            gbs, cgbs = k["bytes"] / k[key] / 1e3, c["bytes"] / c[key] / 1e3
+            k["copy_ceiling"] = {"case": cname, "GB/s": round(cgbs, 1), "frac": round(gbs / cgbs, 4), "time": key}
+
+
 def fold_layouts(kernels):
     """Moves the slot-layout cases ("<case>@<layout>") under their case and
     adds the min and median over all layouts (the case's own included)."""
@@ -1002,15 +1014,7 @@ def main() -> int:
         for name, tag in (("qkv_rope_8192", "perm of 32 blocks, seed 8192"), ("kv_write_16384", "perm of 128 blocks, seed 7")):
             if name in kernels:
                 kernels[name]["slot_layout"] = tag
-        # Each streaming kernel's rate as a fraction of the copy of about its
-        # own traffic (kernel time where both were traced, else event time).
-        for name, cname in COPY_CEILING.items():
-            if name in kernels and cname in kernels:
-                k, c = kernels[name], kernels[cname]
-                key = "kernel_us" if "kernel_us" in k and "kernel_us" in c else "us"
-                gbs, cgbs = k["bytes"] / k[key] / 1e3, c["bytes"] / c[key] / 1e3
-                k["copy_ceiling"] = {"case": cname, "GB/s": round(cgbs, 1), "frac": round(gbs / cgbs, 4),
-                                     "time": key}
+        add_copy_ceilings(kernels)
         fold_layouts(kernels)
 
     # Dominant kernel of the step: the largest share of the step's HBM bytes

@@ -140,6 +140,28 @@ def test_slot_layouts_fold_into_their_case_with_min_and_median():
     assert kernels["kv"]["layouts"]["identity"]["kernel_us"] == 21.0
 
 
+def test_copy_ceiling_compares_with_the_copy_of_about_the_same_traffic():
+    kernels = {"copy_64mb": {"bytes": 64_000_000, "us": 12.0, "kernel_us": 10.0},
+               "copy_128mb": {"bytes": 128_000_000, "us": 22.0},
+               "add_rms_8192x1024": {"bytes": 67_000_000, "us": 12.0, "kernel_us": 11.0},
+               "silu_8192x6144": {"bytes": 151_000_000, "us": 26.0, "kernel_us": 24.0},
+               "rms_8x1024": {"bytes": 34_816, "us": 2.0}}
+    bench.add_copy_ceilings(kernels)
+    c = kernels["add_rms_8192x1024"]["copy_ceiling"]
+    # kernel time on both sides: 67 MB / 11 us against 64 MB / 10 us
+    assert c["case"] == "copy_64mb" and c["time"] == "kernel_us"
+    assert c["GB/s"] == 6400.0 and c["frac"] == round((67e6 / 11.0) / (64e6 / 10.0), 4)
+    # the 128 MiB copy has no kernel time: both sides by event time
+    c = kernels["silu_8192x6144"]["copy_ceiling"]
+    assert c["case"] == "copy_128mb" and c["time"] == "us"
+    assert c["frac"] == round((151e6 / 26.0) / (128e6 / 22.0), 4)
+    assert "copy_ceiling" not in kernels["rms_8x1024"] and "copy_ceiling" not in kernels["copy_64mb"]
+    # no copy case measured: no field
+    alone = {"qkv_rope_8192": {"bytes": 136_000_000, "us": 25.0}}
+    bench.add_copy_ceilings(alone)
+    assert "copy_ceiling" not in alone["qkv_rope_8192"]
+
+
 def test_sweep_slot_layouts_are_distinct_slots_inside_the_cache():
     for tokens, blocks in ((8192, 32), (16384, 128)):
         layouts = bench.slot_layouts(tokens, blocks)
