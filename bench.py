@@ -380,8 +380,8 @@ def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=(), sw
         dsts = [gpu.alloc(rows * H * 2) for _ in range(s)]
         ident = fill.ints(np.arange(rows, dtype=np.int32))
         cases.append(("copy_64mb", f"copy: row gather of {rows} rows of 2 KiB over identity ids",
-                      [lambda i=i, rows=rows, ident=ident, srcs=srcs, dsts=dsts: gpu.embedding(ident, srcs[i], dsts[i], rows, H, rows)
-                       for i in range(s)],
+                      [lambda i=i, rows=rows, ident=ident, srcs=srcs, dsts=dsts:
+                       gpu.embedding(ident, srcs[i], dsts[i], rows, H, rows) for i in range(s)],
                       bytes_embedding(rows, H), rows))
     if want("copy_128mb"):
         rows = 16384
@@ -393,8 +393,9 @@ def kernel_cases(gpu: nvr.Gpu, hip: Hip, fill: Filler, chain: Chain, only=(), sw
         cvc = [gpu.alloc(half) for _ in range(s)]
         cid = fill.ints(np.arange(rows, dtype=np.int32))
         cases.append(("copy_128mb", f"copy: KV write of k, v [{rows},8,128] through identity slots",
-                      [lambda i=i, rows=rows: gpu.kv_write(cks[i], cvs[i], cid, ckc[i], cvc[i], rows, KVH, D, BS,
-                                                           rows // BS) for i in range(s)],
+                      [lambda i=i, rows=rows, cid=cid, cks=cks, cvs=cvs, ckc=ckc, cvc=cvc:
+                       gpu.kv_write(cks[i], cvs[i], cid, ckc[i], cvc[i], rows, KVH, D, BS, rows // BS)
+                       for i in range(s)],
                       bytes_kv_write(rows), rows))
 
     # Paged KV write, k/v [16384, 8, 128] into the per-layer caches of a
@@ -900,7 +901,8 @@ def add_copy_ceilings(kernels):
             k, c = kernels[name], kernels[cname]
             key = "kernel_us" if "kernel_us" in k and "kernel_us" in c else "us"
             gbs, cgbs = k["bytes"] / k[key] / 1e3, c["bytes"] / c[key] / 1e3
-            k["copy_ceiling"] = {"case": cname, "GB/s": round(cgbs, 1), "frac": round(gbs / cgbs, 4), "time": key}
+            k["copy_ceiling"] = {"case": cname, "GB/s": round(cgbs, 1), "frac": round(gbs / cgbs, 4),
+                                 "time": key}
 
 
 def fold_layouts(kernels):
